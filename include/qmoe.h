@@ -1,0 +1,139 @@
+/*
+ * qmoe.h -- C ABI of the MI355X (gfx950) MoE block that replaces the body of
+ * qwen-go's moeMLP.forward.
+ *
+ * The ABI is plain C: handles, host or device pointers, sizes and a status
+ * code.  It carries no HIP or torch types, so a cgo shim can bind it directly.
+ * Citations are to the qwen-go source tree (file:line).
+ *
+ * Layouts (row-major, identical to the reference's safetensors layout):
+ *   router      (E, H)                        model/load.go:419 (mlp.gate.weight)
+ *   gate_up     (E, 2I, H), rows [0,I) gate    model/moe.go:12,59,70-71
+ *               and rows [I,2I) up
+ *   down        (E, H, I)                      model/moe.go:13,60
+ *   shared gate/up (Is, H), down (H, Is)       model/model.go:339-358
+ *   shared_gate (H) f32                        model/moe.go:18,89-93
+ * Formats (qmoe_format):
+ *   QMOE_F32      float32 elements
+ *   QMOE_BF16     uint16 bf16 bit patterns (model/model.go:113-115)
+ *   QMOE_INT8G32  int8 codes (rows, K) + fp16 scales (rows, K/32)
+ *   QMOE_INT4G32  packed bytes (rows, K/2), high nibble = even element,
+ *                 value = nibble - 8, + fp16 scales (rows, K/32)
+ *                 (model/moe.go:134-157; scales are the fp16 form that
+ *                 safetensors F16 files hold, widened exactly)
+ * For stacked experts the scale arrays are (E, rows, K/32).
+ *
+ * Threading: every call on one handle is serialised by a per-handle mutex, so
+ * concurrent Generate goroutines may share a handle.  qmoe_forward_device is
+ * asynchronous on the caller's stream and uses the handle's workspace: calls on
+ * one handle must be ordered on one stream (or synchronised by the caller).
+ */
+#ifndef QMOE_H
+#define QMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    QMOE_OK = 0,
+    QMOE_ERR_INVALID = 1,     /* bad argument: null pointer, dims, T < 0, format */
+    QMOE_ERR_STATE = 2,       /* weights not uploaded, or handle destroyed */
+    QMOE_ERR_NOMEM = 3,       /* device allocation failed */
+    QMOE_ERR_HIP = 4,         /* HIP runtime error (message in qmoe_last_error) */
+    QMOE_ERR_UNSUPPORTED = 5  /* valid but not supported (e.g. E > 1024) */
+} qmoe_status;
+
+typedef enum {
+    QMOE_F32 = 0,
+    QMOE_BF16 = 1,
+    QMOE_INT8G32 = 2,
+    QMOE_INT4G32 = 3
+} qmoe_format;
+
+/* Layer description.  Field meanings follow model/config.go:24-27 and
+ * moeMLP (model/moe.go:10-25). */
+typedef struct {
+    int32_t hidden;        /* H, nEmbed */
+    int32_t n_experts;     /* E, NExperts */
+    int32_t top_k;         /* k, NExpertsPerToken */
+    int32_t moe_inter;     /* I, NMoeMlp */
+    int32_t shared_inter;  /* Is, NSharedExpertMlp; 0 = no shared expert */
+    int32_t select_scope;  /* C in [k, E]: stable-sort the first C probabilities and
+                              take the first k.  0 or k = model/moe.go:45-53 as
+                              written (always experts {0..k-1}, ordered by p);
+                              E = true top-k, ties to the lowest index */
+    int32_t router_fmt;    /* qmoe_format of the router (E, H) */
+    int32_t expert_fmt;    /* qmoe_format of the stacked experts */
+    int32_t shared_fmt;    /* qmoe_format of the shared expert projections */
+    int32_t device;        /* HIP device ordinal */
+} qmoe_desc;
+
+typedef struct qmoe_layer qmoe_layer;
+
+/* newMoeMLP (model/moe.go:27-39): validates the description and allocates the
+ * device weight arrays.  Quantised formats need H and I (and Is) % 32 == 0. */
+qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out);
+
+/* Releases device memory.  Safe on NULL; a handle must not be used after it. */
+void qmoe_destroy(qmoe_layer *layer);
+
+/* Message of the last failing call on this handle (or of the last failing
+ * qmoe_create on this thread when layer is NULL).  Never NULL. */
+const char *qmoe_last_error(const qmoe_layer *layer);
+const char *qmoe_status_string(qmoe_status s);
+
+/* Weight upload from host memory (copied, not retained), as the loader's
+ * loadMLP / installQuant fill moeMLP (model/load.go:415-459, 646-664).
+ * scales: fp16 bit patterns, required for the INT formats, ignored otherwise. */
+qmoe_status qmoe_set_router(qmoe_layer *layer, const void *w, const uint16_t *scales);
+qmoe_status qmoe_set_experts(qmoe_layer *layer, const void *gate_up, const uint16_t *gate_up_scales,
+                             const void *down, const uint16_t *down_scales);
+qmoe_status qmoe_set_shared(qmoe_layer *layer, const void *gate, const uint16_t *gate_scales,
+                            const void *up, const uint16_t *up_scales, const void *down,
+                            const uint16_t *down_scales, const float *shared_gate);
+
+/* Quantises f32 expert weights on the device into the layer's INT8G32 or
+ * INT4G32 expert format: quantizeInt8 / quantizeInt4 (model/moe.go:165-217)
+ * per (rows, K) matrix, then the f32 scale rounded to fp16 (nearest-even).
+ * Codes are computed from the unrounded f32 scale, as the reference does.
+ * gate_up (E, 2I, H) and down (E, H, I) f32 host arrays. */
+qmoe_status qmoe_quantize_experts(qmoe_layer *layer, const float *gate_up, const float *down);
+
+/* Device-pointer quantiser used by qmoe_quantize_experts: n_mat stacked
+ * (rows, cols) f32 matrices -> codes (int8 (rows,cols) or packed int4
+ * (rows,cols/2)) and fp16 scales (rows, cols/32).  bits = 8 or 4.
+ * Asynchronous on stream (hipStream_t; NULL = default stream). */
+qmoe_status qmoe_quantize_device(int32_t bits, const float *d_w, int64_t n_mat, int32_t rows,
+                                 int32_t cols, void *d_codes, uint16_t *d_scales, void *stream);
+
+/* moeMLP.forward (model/moe.go:41-99) for T tokens, host pointers, synchronous.
+ * x (T, H) f32 in; out (T, H) f32 out.  ids (T, k) int32 and weights (T, k) f32
+ * receive the selected experts and renormalised routing weights in rank
+ * order; either may be NULL.  T == 0 is a no-op.  The Go seam calls it with
+ * T = 1 (model/model.go:508-514). */
+qmoe_status qmoe_forward(qmoe_layer *layer, const float *x, int32_t T, float *out, int32_t *ids,
+                         float *weights);
+
+/* Same, on device pointers, asynchronous on stream (hipStream_t; NULL = the
+ * default stream).  No host synchronisation. */
+qmoe_status qmoe_forward_device(qmoe_layer *layer, const float *d_x, int32_t T, float *d_out,
+                                int32_t *d_ids, float *d_weights, void *stream);
+
+/* Exact f32 copy of a stored weight matrix, dequantised on the device as
+ * quantLinear.dequantize does (model/moe.go:134-157); bf16 widened as bf16f32.
+ * which: 0 expert gate_up (2I, H), 1 expert down (H, I), 2 router (E, H),
+ *        3 shared gate (Is, H), 4 shared up (Is, H), 5 shared down (H, Is).
+ * expert is ignored for which >= 2.  out is a host array of rows*cols f32. */
+qmoe_status qmoe_dequant_debug(qmoe_layer *layer, int32_t which, int32_t expert, float *out);
+
+/* Bytes of device memory held by the handle (weights + workspace). */
+int64_t qmoe_device_bytes(const qmoe_layer *layer);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,508 @@
+// layer.hip -- the C ABI (include/qmoe.h): handle, weight upload and the
+// forward orchestration of the MoE block on one gfx950 device.
+//
+// Forward (model/moe.go:41-99 for T tokens at once):
+//   1. router logits, exact sequential f32 per (token, expert)   router.hip
+//   2. softmax + selection over the first C + renormalisation     router.hip
+//   3. expert gate_up GEMV + SwiGLU (+ shared expert gate_up and
+//      its sigmoid gate)                                          gemv.hip
+//   4. expert down GEMV + weighted combine in rank order + shared  gemv.hip
+// All kernels run on one stream; the host-pointer entry copies x in and out
+// around them and synchronises, as the cgo seam needs.
+#include "../../include/qmoe.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <vector>
+
+using namespace qmoe;
+
+namespace {
+
+thread_local std::string g_create_error = "no error";
+
+struct DevBuf {
+  void *p = nullptr;
+  size_t n = 0;
+};
+
+}  // namespace
+
+struct qmoe_layer {
+  qmoe_desc d{};
+  int scope = 0;
+  std::mutex mu;
+  std::string err = "no error";
+  bool destroyed = false;
+  hipStream_t stream = nullptr;
+  std::vector<DevBuf> owned;
+  int64_t weight_bytes = 0;
+
+  DevMat router, gu, dn, sgate, sup, sdown;
+  float *shared_gate = nullptr;
+  bool has_router = false, has_experts = false, has_shared = false;
+
+  // workspace, sized for ws_T tokens
+  int ws_T = 0;
+  DevBuf ws;
+  float *logits = nullptr, *wts = nullptr, *act = nullptr, *act_s = nullptr, *sg = nullptr;
+  float *xbuf = nullptr, *obuf = nullptr;
+  int32_t *ids = nullptr;
+};
+
+namespace {
+
+qmoe_status fail(qmoe_layer *l, qmoe_status s, const std::string &msg) {
+  if (l) l->err = msg;
+  else g_create_error = msg;
+  return s;
+}
+
+qmoe_status hip_fail(qmoe_layer *l, hipError_t e, const char *what) {
+  return fail(l, QMOE_ERR_HIP, std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+}
+
+#define HIP_TRY(l, expr, what)                    \
+  do {                                            \
+    hipError_t _e = (expr);                       \
+    if (_e != hipSuccess) return hip_fail(l, _e, what); \
+  } while (0)
+
+bool valid_fmt(int f) { return f >= QMOE_F32 && f <= QMOE_INT4G32; }
+
+// Allocates a (n_mat x rows x cols) stack in fmt plus its scales.
+qmoe_status alloc_mat(qmoe_layer *l, DevMat &m, int fmt, int64_t n_mat, int rows, int cols) {
+  m.fmt = fmt;
+  m.rows = rows;
+  m.cols = cols;
+  m.mat_bytes = fmt_matrix_bytes(fmt, rows, cols);
+  m.mat_scales = fmt_quant(fmt) ? (int64_t)rows * (cols / kGroup) : 0;
+  DevBuf b;
+  b.n = (size_t)(m.mat_bytes * n_mat);
+  if (hipMalloc(&b.p, b.n) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(l, QMOE_ERR_NOMEM, "hipMalloc of " + std::to_string(b.n) + " weight bytes failed");
+  }
+  l->owned.push_back(b);
+  l->weight_bytes += (int64_t)b.n;
+  m.w = (const uint8_t *)b.p;
+  m.s = nullptr;
+  if (m.mat_scales) {
+    DevBuf sb;
+    sb.n = (size_t)(m.mat_scales * n_mat) * sizeof(uint16_t);
+    if (hipMalloc(&sb.p, sb.n) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(l, QMOE_ERR_NOMEM, "hipMalloc of " + std::to_string(sb.n) + " scale bytes failed");
+    }
+    l->owned.push_back(sb);
+    l->weight_bytes += (int64_t)sb.n;
+    m.s = (const uint16_t *)sb.p;
+  }
+  return QMOE_OK;
+}
+
+void free_all(qmoe_layer *l) {
+  for (auto &b : l->owned)
+    if (b.p) (void)hipFree(b.p);
+  l->owned.clear();
+  if (l->ws.p) (void)hipFree(l->ws.p);
+  l->ws = DevBuf{};
+  l->ws_T = 0;
+  if (l->stream) (void)hipStreamDestroy(l->stream);
+  l->stream = nullptr;
+}
+
+qmoe_status upload(qmoe_layer *l, const DevMat &m, int64_t n_mat, const void *w, const uint16_t *s) {
+  if (!w) return fail(l, QMOE_ERR_INVALID, "null weight pointer");
+  if (fmt_quant(m.fmt) && !s) return fail(l, QMOE_ERR_INVALID, "null scale pointer for a quantised format");
+  HIP_TRY(l, hipMemcpy((void *)m.w, w, (size_t)(m.mat_bytes * n_mat), hipMemcpyHostToDevice), "weight upload");
+  if (fmt_quant(m.fmt))
+    HIP_TRY(l, hipMemcpy((void *)m.s, s, (size_t)(m.mat_scales * n_mat) * sizeof(uint16_t), hipMemcpyHostToDevice),
+            "scale upload");
+  return QMOE_OK;
+}
+
+qmoe_status enter(qmoe_layer *l) {
+  if (!l) return QMOE_ERR_INVALID;
+  if (l->destroyed) return fail(l, QMOE_ERR_STATE, "handle used after qmoe_destroy");
+  HIP_TRY(l, hipSetDevice(l->d.device), "hipSetDevice");
+  return QMOE_OK;
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
+  if (T <= l->ws_T) return QMOE_OK;
+  const qmoe_desc &d = l->d;
+  int nT = std::max(T, 64);
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes); return o; };
+  size_t o_logits = take((size_t)nT * d.n_experts * 4);
+  size_t o_ids = take((size_t)nT * d.top_k * 4);
+  size_t o_wts = take((size_t)nT * d.top_k * 4);
+  size_t o_act = take((size_t)nT * d.top_k * d.moe_inter * 4);
+  size_t o_acts = take((size_t)nT * std::max(d.shared_inter, 1) * 4);
+  size_t o_sg = take((size_t)nT * 4);
+  size_t o_x = take((size_t)nT * d.hidden * 4);
+  size_t o_o = take((size_t)nT * d.hidden * 4);
+  // Pending work of earlier calls may still read the old workspace.
+  if (user_stream) HIP_TRY(l, hipStreamSynchronize(user_stream), "hipStreamSynchronize");
+  HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+  if (l->ws.p) (void)hipFree(l->ws.p);
+  l->ws = DevBuf{};
+  l->ws_T = 0;
+  if (hipMalloc(&l->ws.p, off) != hipSuccess) {
+    (void)hipGetLastError();
+    l->ws.p = nullptr;
+    return fail(l, QMOE_ERR_NOMEM, "hipMalloc of " + std::to_string(off) + " workspace bytes failed");
+  }
+  l->ws.n = off;
+  char *b = (char *)l->ws.p;
+  l->logits = (float *)(b + o_logits);
+  l->ids = (int32_t *)(b + o_ids);
+  l->wts = (float *)(b + o_wts);
+  l->act = (float *)(b + o_act);
+  l->act_s = (float *)(b + o_acts);
+  l->sg = (float *)(b + o_sg);
+  l->xbuf = (float *)(b + o_x);
+  l->obuf = (float *)(b + o_o);
+  l->ws_T = nT;
+  return QMOE_OK;
+}
+
+qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, int32_t *d_ids,
+                        float *d_w, hipStream_t st) {
+  const qmoe_desc &d = l->d;
+  if (!l->has_router || !l->has_experts || (d.shared_inter > 0 && !l->has_shared))
+    return fail(l, QMOE_ERR_STATE, "weights not uploaded (router, experts and shared expert are required)");
+  int32_t *ids = d_ids ? d_ids : l->ids;
+  float *wts = d_w ? d_w : l->wts;
+  const int H = d.hidden, E = d.n_experts, k = d.top_k, I = d.moe_inter, Is = d.shared_inter;
+
+  HIP_TRY(l, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
+  HIP_TRY(l, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st), "softmax/select launch");
+
+  GateUpArgs g{};
+  g.x = d_x;
+  g.ids = ids;
+  g.T = T;
+  g.k = k;
+  g.H = H;
+  g.I = I;
+  g.gate = l->gu.w;
+  g.up = l->gu.w + fmt_matrix_bytes(l->gu.fmt, I, H);
+  g.gate_s = l->gu.s;
+  g.up_s = l->gu.s ? l->gu.s + (int64_t)I * (H / kGroup) : nullptr;
+  g.expert_bytes = l->gu.mat_bytes;
+  g.expert_scales = l->gu.mat_scales;
+  g.fmt = l->gu.fmt;
+  g.act = l->act;
+  HIP_TRY(l, launch_gate_up_gemv(g, st), "gate_up launch");
+
+  if (Is > 0) {
+    GateUpArgs s{};
+    s.x = d_x;
+    s.ids = nullptr;
+    s.T = T;
+    s.k = 1;
+    s.H = H;
+    s.I = Is;
+    s.gate = l->sgate.w;
+    s.up = l->sup.w;
+    s.gate_s = l->sgate.s;
+    s.up_s = l->sup.s;
+    s.expert_bytes = 0;
+    s.expert_scales = 0;
+    s.fmt = l->sgate.fmt;
+    s.act = l->act_s;
+    s.shared_gate = l->shared_gate;
+    s.sg = l->sg;
+    HIP_TRY(l, launch_gate_up_gemv(s, st), "shared gate_up launch");
+  }
+
+  DownArgs a{};
+  a.act = l->act;
+  a.ids = ids;
+  a.weights = wts;
+  a.T = T;
+  a.k = k;
+  a.H = H;
+  a.I = I;
+  a.down = l->dn.w;
+  a.down_s = l->dn.s;
+  a.expert_bytes = l->dn.mat_bytes;
+  a.expert_scales = l->dn.mat_scales;
+  a.fmt = l->dn.fmt;
+  a.act_s = l->act_s;
+  a.sg = l->sg;
+  a.Is = Is;
+  a.sdown = Is > 0 ? l->sdown.w : nullptr;
+  a.sdown_s = Is > 0 ? l->sdown.s : nullptr;
+  a.sfmt = Is > 0 ? l->sdown.fmt : l->dn.fmt;
+  a.out = d_out;
+  HIP_TRY(l, launch_down_gemv(a, st), "down launch");
+  return QMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *qmoe_status_string(qmoe_status s) {
+  switch (s) {
+  case QMOE_OK: return "ok";
+  case QMOE_ERR_INVALID: return "invalid argument";
+  case QMOE_ERR_STATE: return "invalid state";
+  case QMOE_ERR_NOMEM: return "out of device memory";
+  case QMOE_ERR_HIP: return "HIP runtime error";
+  case QMOE_ERR_UNSUPPORTED: return "unsupported configuration";
+  }
+  return "unknown status";
+}
+
+const char *qmoe_last_error(const qmoe_layer *layer) {
+  if (!layer) return g_create_error.c_str();
+  return layer->err.c_str();
+}
+
+qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
+  if (!desc || !out) return fail(nullptr, QMOE_ERR_INVALID, "null desc or out pointer");
+  *out = nullptr;
+  const qmoe_desc d = *desc;
+  if (d.hidden <= 0 || d.n_experts <= 0 || d.top_k <= 0 || d.moe_inter <= 0 || d.shared_inter < 0)
+    return fail(nullptr, QMOE_ERR_INVALID, "dimensions must be positive (shared_inter >= 0)");
+  if (d.top_k > d.n_experts) return fail(nullptr, QMOE_ERR_INVALID, "top_k > n_experts");
+  if (d.select_scope != 0 && (d.select_scope < d.top_k || d.select_scope > d.n_experts))
+    return fail(nullptr, QMOE_ERR_INVALID, "select_scope must be 0 or in [top_k, n_experts]");
+  if (!valid_fmt(d.router_fmt) || !valid_fmt(d.expert_fmt) || !valid_fmt(d.shared_fmt))
+    return fail(nullptr, QMOE_ERR_INVALID, "unknown weight format");
+  if (d.hidden % 32 || d.moe_inter % 32 || d.shared_inter % 32)
+    return fail(nullptr, QMOE_ERR_UNSUPPORTED, "hidden, moe_inter and shared_inter must be multiples of 32");
+  if (d.n_experts > 1024 || d.top_k > 64)
+    return fail(nullptr, QMOE_ERR_UNSUPPORTED, "n_experts > 1024 or top_k > 64");
+  if (d.hidden > 16384)
+    return fail(nullptr, QMOE_ERR_UNSUPPORTED, "hidden > 16384");
+  if ((int64_t)(d.top_k * d.moe_inter + d.shared_inter) * 4 > 64 * 1024)
+    return fail(nullptr, QMOE_ERR_UNSUPPORTED, "top_k * moe_inter + shared_inter exceeds 16384 floats");
+  int ndev = 0;
+  hipError_t e = hipGetDeviceCount(&ndev);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "hipGetDeviceCount");
+  if (d.device < 0 || d.device >= ndev) return fail(nullptr, QMOE_ERR_INVALID, "device ordinal out of range");
+  e = hipSetDevice(d.device);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
+
+  qmoe_layer *l = new qmoe_layer();
+  l->d = d;
+  l->scope = d.select_scope == 0 ? d.top_k : d.select_scope;
+  e = hipStreamCreate(&l->stream);
+  if (e != hipSuccess) {
+    delete l;
+    return hip_fail(nullptr, e, "hipStreamCreate");
+  }
+  qmoe_status s;
+  const int H = d.hidden, E = d.n_experts, I = d.moe_inter, Is = d.shared_inter;
+  if ((s = alloc_mat(l, l->router, d.router_fmt, 1, E, H)) != QMOE_OK ||
+      (s = alloc_mat(l, l->gu, d.expert_fmt, E, 2 * I, H)) != QMOE_OK ||
+      (s = alloc_mat(l, l->dn, d.expert_fmt, E, H, I)) != QMOE_OK ||
+      (Is > 0 && ((s = alloc_mat(l, l->sgate, d.shared_fmt, 1, Is, H)) != QMOE_OK ||
+                  (s = alloc_mat(l, l->sup, d.shared_fmt, 1, Is, H)) != QMOE_OK ||
+                  (s = alloc_mat(l, l->sdown, d.shared_fmt, 1, H, Is)) != QMOE_OK))) {
+    g_create_error = l->err;
+    free_all(l);
+    delete l;
+    return s;
+  }
+  if (Is > 0) {
+    DevBuf b;
+    b.n = (size_t)H * 4;
+    if (hipMalloc(&b.p, b.n) != hipSuccess) {
+      (void)hipGetLastError();
+      free_all(l);
+      delete l;
+      return fail(nullptr, QMOE_ERR_NOMEM, "hipMalloc of shared gate failed");
+    }
+    l->owned.push_back(b);
+    l->weight_bytes += (int64_t)b.n;
+    l->shared_gate = (float *)b.p;
+  }
+  *out = l;
+  return QMOE_OK;
+}
+
+void qmoe_destroy(qmoe_layer *layer) {
+  if (!layer) return;
+  {
+    std::lock_guard<std::mutex> g(layer->mu);
+    if (layer->destroyed) return;
+    (void)hipSetDevice(layer->d.device);
+    if (layer->stream) (void)hipStreamSynchronize(layer->stream);
+    free_all(layer);
+    layer->destroyed = true;
+  }
+  delete layer;
+}
+
+qmoe_status qmoe_set_router(qmoe_layer *l, const void *w, const uint16_t *scales) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if ((s = upload(l, l->router, 1, w, scales)) != QMOE_OK) return s;
+  l->has_router = true;
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_set_experts(qmoe_layer *l, const void *gate_up, const uint16_t *gate_up_scales,
+                             const void *down, const uint16_t *down_scales) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  const int E = l->d.n_experts;
+  if ((s = upload(l, l->gu, E, gate_up, gate_up_scales)) != QMOE_OK) return s;
+  if ((s = upload(l, l->dn, E, down, down_scales)) != QMOE_OK) return s;
+  l->has_experts = true;
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_set_shared(qmoe_layer *l, const void *gate, const uint16_t *gate_scales, const void *up,
+                            const uint16_t *up_scales, const void *down, const uint16_t *down_scales,
+                            const float *shared_gate) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (l->d.shared_inter <= 0) return fail(l, QMOE_ERR_STATE, "layer has no shared expert (shared_inter == 0)");
+  if (!shared_gate) return fail(l, QMOE_ERR_INVALID, "null shared_gate");
+  if ((s = upload(l, l->sgate, 1, gate, gate_scales)) != QMOE_OK) return s;
+  if ((s = upload(l, l->sup, 1, up, up_scales)) != QMOE_OK) return s;
+  if ((s = upload(l, l->sdown, 1, down, down_scales)) != QMOE_OK) return s;
+  HIP_TRY(l, hipMemcpy(l->shared_gate, shared_gate, (size_t)l->d.hidden * 4, hipMemcpyHostToDevice),
+          "shared gate upload");
+  l->has_shared = true;
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_quantize_device(int32_t bits, const float *d_w, int64_t n_mat, int32_t rows, int32_t cols,
+                                 void *d_codes, uint16_t *d_scales, void *stream) {
+  if ((bits != 8 && bits != 4) || !d_w || !d_codes || !d_scales || n_mat < 0 || rows < 0 || cols <= 0 ||
+      cols % 32)
+    return fail(nullptr, QMOE_ERR_INVALID, "qmoe_quantize_device: bad arguments");
+  hipError_t e = launch_quantize(bits, d_w, n_mat * rows, cols, (uint8_t *)d_codes, d_scales,
+                                 (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "quantize launch");
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_quantize_experts(qmoe_layer *l, const float *gate_up, const float *down) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (!gate_up || !down) return fail(l, QMOE_ERR_INVALID, "null weight pointer");
+  const int bits = l->d.expert_fmt == QMOE_INT8G32 ? 8 : l->d.expert_fmt == QMOE_INT4G32 ? 4 : 0;
+  if (!bits) return fail(l, QMOE_ERR_STATE, "expert format is not INT8G32 or INT4G32");
+  const int E = l->d.n_experts;
+  // Stage at most ~256 MiB of f32 at a time.
+  for (int which = 0; which < 2; which++) {
+    const DevMat &m = which == 0 ? l->gu : l->dn;
+    const float *src = which == 0 ? gate_up : down;
+    const int64_t per = (int64_t)m.rows * m.cols;
+    int64_t chunk = std::max<int64_t>(1, (256ll << 20) / (per * 4));
+    chunk = std::min<int64_t>(chunk, E);
+    float *tmp = nullptr;
+    HIP_TRY(l, hipMalloc(&tmp, (size_t)(chunk * per * 4)), "hipMalloc quantiser staging");
+    for (int64_t e0 = 0; e0 < E; e0 += chunk) {
+      int64_t n = std::min<int64_t>(chunk, E - e0);
+      hipError_t err = hipMemcpy(tmp, src + e0 * per, (size_t)(n * per * 4), hipMemcpyHostToDevice);
+      if (err == hipSuccess)
+        err = launch_quantize(bits, tmp, n * m.rows, m.cols, (uint8_t *)m.w + e0 * m.mat_bytes,
+                              (uint16_t *)m.s + e0 * m.mat_scales, l->stream);
+      if (err == hipSuccess) err = hipStreamSynchronize(l->stream);
+      if (err != hipSuccess) {
+        (void)hipFree(tmp);
+        return hip_fail(l, err, "expert quantisation");
+      }
+    }
+    (void)hipFree(tmp);
+  }
+  l->has_experts = true;
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_forward_device(qmoe_layer *l, const float *d_x, int32_t T, float *d_out, int32_t *d_ids,
+                                float *d_weights, void *stream) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (T < 0) return fail(l, QMOE_ERR_INVALID, "T < 0");
+  if (T == 0) return QMOE_OK;
+  if (!d_x || !d_out) return fail(l, QMOE_ERR_INVALID, "null x or out pointer");
+  if ((int64_t)T * l->d.top_k > 65535) return fail(l, QMOE_ERR_UNSUPPORTED, "T * top_k > 65535");
+  hipStream_t st = (hipStream_t)stream;
+  if ((s = ensure_workspace(l, T, st)) != QMOE_OK) return s;
+  return run_forward(l, d_x, T, d_out, d_ids, d_weights, st);
+}
+
+qmoe_status qmoe_forward(qmoe_layer *l, const float *x, int32_t T, float *out, int32_t *ids, float *weights) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (T < 0) return fail(l, QMOE_ERR_INVALID, "T < 0");
+  if (T == 0) return QMOE_OK;
+  if (!x || !out) return fail(l, QMOE_ERR_INVALID, "null x or out pointer");
+  if ((int64_t)T * l->d.top_k > 65535) return fail(l, QMOE_ERR_UNSUPPORTED, "T * top_k > 65535");
+  if ((s = ensure_workspace(l, T, nullptr)) != QMOE_OK) return s;
+  const size_t xb = (size_t)T * l->d.hidden * 4;
+  HIP_TRY(l, hipMemcpyAsync(l->xbuf, x, xb, hipMemcpyHostToDevice, l->stream), "x upload");
+  if ((s = run_forward(l, l->xbuf, T, l->obuf, l->ids, l->wts, l->stream)) != QMOE_OK) return s;
+  HIP_TRY(l, hipMemcpyAsync(out, l->obuf, xb, hipMemcpyDeviceToHost, l->stream), "out download");
+  const size_t kb = (size_t)T * l->d.top_k * 4;
+  if (ids) HIP_TRY(l, hipMemcpyAsync(ids, l->ids, kb, hipMemcpyDeviceToHost, l->stream), "ids download");
+  if (weights) HIP_TRY(l, hipMemcpyAsync(weights, l->wts, kb, hipMemcpyDeviceToHost, l->stream), "weights download");
+  HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_dequant_debug(qmoe_layer *l, int32_t which, int32_t expert, float *out) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (!out) return fail(l, QMOE_ERR_INVALID, "null out pointer");
+  const DevMat *m = nullptr;
+  int64_t index = 0;
+  switch (which) {
+  case 0: m = &l->gu; index = expert; break;
+  case 1: m = &l->dn; index = expert; break;
+  case 2: m = &l->router; break;
+  case 3: m = &l->sgate; break;
+  case 4: m = &l->sup; break;
+  case 5: m = &l->sdown; break;
+  default: return fail(l, QMOE_ERR_INVALID, "which must be in [0, 5]");
+  }
+  if (which >= 3 && l->d.shared_inter <= 0) return fail(l, QMOE_ERR_STATE, "layer has no shared expert");
+  if (which <= 1 && (expert < 0 || expert >= l->d.n_experts))
+    return fail(l, QMOE_ERR_INVALID, "expert out of range");
+  const size_t n = (size_t)m->rows * m->cols;
+  float *tmp = nullptr;
+  HIP_TRY(l, hipMalloc(&tmp, n * 4), "hipMalloc dequant staging");
+  hipError_t e = launch_dequantize(*m, index, tmp, l->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(out, tmp, n * 4, hipMemcpyDeviceToHost, l->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
+  (void)hipFree(tmp);
+  if (e != hipSuccess) return hip_fail(l, e, "dequant_debug");
+  return QMOE_OK;
+}
+
+int64_t qmoe_device_bytes(const qmoe_layer *l) {
+  if (!l) return 0;
+  return l->weight_bytes + (int64_t)l->ws.n;
+}
+
+}  // extern "C"

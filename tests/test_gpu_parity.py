@@ -1,0 +1,203 @@
+"""GPU parity: libqmoe.so (HIP, gfx950) against the CPU oracle.
+
+Bars (written into each assertion):
+  * expert ids: exact, in rank order (the router sums each logit sequentially
+    in f32 exactly as model/moe.go does);
+  * routing weights: exact up to the last bit of exp (tolerance 1e-6 relative);
+  * dequantised weights and device-quantised codes/scales: bit-exact;
+  * layer output on the GEMV path (f32 activations): normwise relative error
+    max_j|y-y_ref| / max_j|y_ref| <= 1e-3 per token.
+Every test prints the case it runs before touching the GPU.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import qmoe
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+
+
+def rel_err(out, ref):
+    return (np.abs(out - ref).max(axis=1) / np.maximum(np.abs(ref).max(axis=1), 1e-30)).max()
+
+
+def announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def check_layer(cfg, hw, x, tol=TOL_F32, scope=None):
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(x)
+    finally:
+        layer.close()
+    ref, rids, rw = oracle.OracleLayer(hw, scope=scope).forward(x)
+    assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
+    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
+    err = rel_err(out, ref)
+    assert err <= tol, f"normwise relative error {err:.3e} > {tol}"
+    return err
+
+
+# ------------------------------------------------------------ quantiser
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_device_quantizer_bitexact(bits):
+    import torch
+    announce(f"device quantiser int{bits}")
+    rng = np.random.default_rng(11 + bits)
+    n_mat, rows, cols = 3, 40, 256
+    w = (rng.standard_normal((n_mat, rows, cols), dtype=np.float32) * np.float32(0.02))
+    w[0, 0, :32] = 0.0                      # amax 0 -> scale floored at 1e-8
+    w[0, 1, :32] = np.float32(1e-12)        # tiny group
+    # exact half-way points: w/s = k + 0.5 must round away from zero
+    s = np.float32(1.0) / np.float32(127.0) if bits == 8 else np.float32(1.0) / np.float32(7.0)
+    w[1, 2, :32] = 0.0
+    w[1, 2, 0] = 1.0
+    w[1, 2, 1] = np.float32(2.5) * s
+    w[1, 2, 2] = -np.float32(2.5) * s
+    codes_ref, scales_ref = oracle.quantize_f16(bits, w)
+    dw = torch.from_numpy(w.reshape(-1).copy()).cuda()
+    codes = torch.empty(codes_ref.size, dtype=torch.uint8, device="cuda")
+    scales = torch.empty(scales_ref.size, dtype=torch.int16, device="cuda")
+    qmoe.quantize_device(bits, dw.data_ptr(), n_mat, rows, cols, codes.data_ptr(), scales.data_ptr(),
+                         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    c = codes.cpu().numpy()
+    assert np.array_equal(c, codes_ref.reshape(-1).view(np.uint8))
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), scales_ref.reshape(-1))
+
+
+@pytest.mark.parametrize("fmt", [qmoe.INT8G32, qmoe.INT4G32, qmoe.BF16, qmoe.F32])
+def test_dequant_debug_bitexact(fmt):
+    announce(f"dequant_debug fmt={qmoe.FORMAT_NAMES[fmt]}")
+    cfg = qmoe.LayerConfig(256, 6, 2, 96, 64, 0, fmt, fmt, fmt, "dq")
+    hw = qmoe.synthetic_weights(cfg, 5, quantizer=oracle.host_quantizer)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        bits = 8 if fmt == qmoe.INT8G32 else 4
+
+        def ref(w, s16, rows, cols):
+            if fmt == qmoe.F32:
+                return w.reshape(rows, cols)
+            if fmt == qmoe.BF16:
+                return qmoe.bf16_bits_to_f32(w).reshape(rows, cols)
+            return oracle.dequantize(bits, w, oracle.f16_to_f32(s16), rows, cols)
+
+        H, I, E, Is = cfg.hidden, cfg.moe_inter, cfg.n_experts, cfg.shared_inter
+        for e in (0, E - 1):
+            gu_s = hw.gate_up_s[e] if hw.gate_up_s is not None else None
+            dn_s = hw.down_s[e] if hw.down_s is not None else None
+            for which, w, s, rows, cols in ((0, hw.gate_up[e], gu_s, 2 * I, H), (1, hw.down[e], dn_s, H, I)):
+                got = layer.dequant(which, e)
+                assert np.array_equal(got.view(np.uint32), ref(w, s, rows, cols).view(np.uint32))
+        cases = ((2, hw.router, hw.router_s, E, H), (3, hw.sh_gate, hw.sh_gate_s, Is, H),
+                 (4, hw.sh_up, hw.sh_up_s, Is, H), (5, hw.sh_down, hw.sh_down_s, H, Is))
+        for which, w, s, rows, cols in cases:
+            got = layer.dequant(which)
+            assert np.array_equal(got.view(np.uint32), ref(w, s, rows, cols).view(np.uint32))
+    finally:
+        layer.close()
+
+
+# --------------------------------------------------------------- layers
+
+@pytest.mark.parametrize("scope", ["k", "E"])
+def test_toy_layer(scope):
+    cfg = qmoe.CONFIGS["toy"]
+    if scope == "E":
+        cfg = cfg.with_(select_scope=cfg.n_experts)
+    announce(f"toy layer T=16 scope={scope}")
+    hw = qmoe.synthetic_weights(cfg, 1, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, 16, 1)
+    check_layer(cfg, hw, x)
+
+
+SMALL = [
+    # (router, experts, shared, shared_inter, scope)
+    (qmoe.F32, qmoe.F32, qmoe.F32, 0, 0),
+    (qmoe.BF16, qmoe.BF16, qmoe.BF16, 64, 0),
+    (qmoe.BF16, qmoe.BF16, qmoe.BF16, 0, 16),
+    (qmoe.INT8G32, qmoe.INT8G32, qmoe.INT4G32, 96, 12),
+    (qmoe.INT4G32, qmoe.INT4G32, qmoe.INT8G32, 64, 16),
+    (qmoe.F32, qmoe.INT4G32, qmoe.F32, 32, 16),
+]
+
+
+@pytest.mark.parametrize("fmts", SMALL, ids=lambda f: "-".join(map(str, f)))
+@pytest.mark.parametrize("T", [1, 3, 37])
+def test_small_layers(fmts, T):
+    rf, ef, sf, Is, scope = fmts
+    cfg = qmoe.LayerConfig(320, 16, 4, 160, Is, scope, rf, ef, sf, "small")
+    announce(f"small layer fmts={fmts} T={T}")
+    hw = qmoe.synthetic_weights(cfg, 100 + T, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, T, 100 + T)
+    check_layer(cfg, hw, x)
+
+
+@pytest.fixture(scope="module")
+def qwen3_bf16():
+    cfg = qmoe.CONFIGS["qwen3_30b_a3b"]
+    return cfg, qmoe.synthetic_weights(cfg, 2026, quantizer=oracle.host_quantizer)
+
+
+@pytest.mark.parametrize("T", [1, 8])
+@pytest.mark.parametrize("scope", ["k", "E"])
+def test_qwen3_30b_a3b_decode(qwen3_bf16, T, scope):
+    cfg, hw = qwen3_bf16
+    if scope == "E":
+        cfg = cfg.with_(select_scope=cfg.n_experts)
+        hw.cfg = cfg
+    announce(f"qwen3-30b-a3b bf16 T={T} scope={scope}")
+    x = qmoe.synthetic_tokens(cfg, T, 2026 + T)
+    try:
+        check_layer(cfg, hw, x)
+    finally:
+        hw.cfg = qmoe.CONFIGS["qwen3_30b_a3b"]
+
+
+def test_qwen3_30b_a3b_int8_decode():
+    cfg = qmoe.CONFIGS["qwen3_30b_a3b_int8"].with_(select_scope=128)
+    announce("qwen3-30b-a3b int8g32 T=1 scope=E")
+    hw = qmoe.synthetic_weights(cfg, 77, quantizer=qmoe.device_quantizer)
+    x = qmoe.synthetic_tokens(cfg, 1, 77)
+    check_layer(cfg, hw, x)
+
+
+def test_qwen3_next_int4_decode():
+    cfg = qmoe.CONFIGS["qwen3_next"].with_(select_scope=512)
+    announce("qwen3-next int4g32 + shared T=1 scope=E")
+    hw = qmoe.synthetic_weights(cfg, 99, quantizer=qmoe.device_quantizer)
+    x = qmoe.synthetic_tokens(cfg, 2, 99)
+    check_layer(cfg, hw, x)
+
+
+# ----------------------------------------------------------- contract
+
+def test_contract_errors():
+    announce("C ABI error paths")
+    cfg = qmoe.LayerConfig(256, 8, 2, 64, 0, 0, qmoe.BF16, qmoe.BF16, qmoe.BF16, "errs")
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        x = np.zeros((1, 256), np.float32)
+        with pytest.raises(qmoe.QmoeError) as ei:
+            layer.forward(x)  # no weights yet
+        assert ei.value.status == 2
+        hw = qmoe.synthetic_weights(cfg, 1, quantizer=oracle.host_quantizer)
+        hw.upload(layer)
+        out, ids, w = layer.forward(np.zeros((0, 256), np.float32))
+        assert out.shape == (0, 256)
+        st = layer.lib.qmoe_forward(layer.h, None, 1, None, None, None)
+        assert st == 1
+        with pytest.raises(qmoe.QmoeError):
+            layer.set_shared(None, None, None, None, None, None, None)
+        with pytest.raises(qmoe.QmoeError):
+            layer.dequant(0, 99)
+    finally:
+        layer.close()
+    layer.close()  # idempotent
