@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""MoE-layer throughput on one MI355X through the C ABI (libqmoe.so).
+
+Default workload: the Qwen3-30B-A3B-shaped MoE layer (H=2048, E=128, top-8,
+I=768, bf16 weights ~ N(0, 0.02)) at decode, T=1 token per step, true top-8 of
+128 (selection scope C=E), x ~ N(0, 1).  One step = one forward of the layer
+over one batch of T tokens whose x already sits in HBM.
+
+Honest bandwidth: the layer's weights are uploaded into several distinct copies
+and the steps rotate through them, so each round of copies reads more than
+2 x 256 MB (the Infinity Cache) of weights.
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel's algorithmic bytes per launch divided by
+                its average duration, timed with HIP events recorded on the
+                kernel's own stream during the timed region;
+  cpu_baseline  the CPU oracle (a C restatement of model/moe.go, the Go
+                reference cannot run here) on a bounded sample of the same
+                workload on this host's cores.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen-go_amd"))
+
+import qmoe  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+WORKLOADS = {
+    # name: (config key, T, scope, description)
+    "decode": ("qwen3_30b_a3b", 1, "E", "qwen3-30b-a3b moe layer decode T=1, bf16 weights, top-8 of 128"),
+    "decode8": ("qwen3_30b_a3b", 8, "E", "qwen3-30b-a3b moe layer decode T=8, bf16 weights, top-8 of 128"),
+    "int8_decode": ("qwen3_30b_a3b_int8", 1, "E",
+                    "qwen3-30b-a3b moe layer decode T=1, int8 group-32 experts, top-8 of 128"),
+    "next_decode": ("qwen3_next", 1, "E",
+                    "qwen3-next moe layer decode T=1, int4 group-32 experts + gated shared expert, top-10 of 512"),
+    "toy": ("toy", 16, "k", "toy moe layer T=16, f32, first-2 of 8 (reference selection)"),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default="decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0 = auto)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=2026)
+    return ap.parse_args()
+
+
+def stage_bytes(cfg, T, ids):
+    """Algorithmic HBM bytes of each kernel for one forward with routing ids."""
+    H, E, k, I, Is = cfg.hidden, cfg.n_experts, cfg.top_k, cfg.moe_inter, cfg.shared_inter
+    touched = len(np.unique(ids))
+    wb = qmoe.weight_bytes
+    b = {
+        qmoe.STAGE_ROUTER: wb(cfg.router_fmt, E, H) + T * H * 4 + T * E * 4,
+        qmoe.STAGE_SELECT: T * E * 4 + T * k * 8,
+        qmoe.STAGE_GATE_UP: touched * wb(cfg.expert_fmt, 2 * I, H) + T * H * 4 + T * k * I * 4,
+        qmoe.STAGE_DOWN: touched * wb(cfg.expert_fmt, H, I) + T * k * I * 4 + T * k * 8 + T * H * 4,
+    }
+    if Is:
+        b[qmoe.STAGE_SHARED_GATE_UP] = 2 * wb(cfg.shared_fmt, Is, H) + H * 4 + T * H * 4 + T * Is * 4 + T * 4
+        b[qmoe.STAGE_DOWN] += wb(cfg.shared_fmt, H, Is) + T * Is * 4 + T * 4
+    # decode: one kernel reads the routed (and shared) gate_up and down weights,
+    # x and the router partials, and accumulates out
+    b[qmoe.STAGE_FUSED] = (touched * (wb(cfg.expert_fmt, 2 * I, H) + wb(cfg.expert_fmt, H, I)) + T * H * 4
+                           + T * E * 16 + T * H * 4)
+    if Is:
+        b[qmoe.STAGE_FUSED] += 2 * wb(cfg.shared_fmt, Is, H) + wb(cfg.shared_fmt, H, Is) + H * 4
+    return b
+
+
+def cpu_baseline(hw, cfg, T, scope, xs, budget_s):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    threads = min(os.cpu_count() or 1, 8)
+    ol = oracle.OracleLayer(hw, scope=scope, threads=threads)
+    x = xs[0][:T]
+    t0 = time.perf_counter()
+    ol.forward(x)
+    one = time.perf_counter() - t0
+    reps = max(2, min(400, int(budget_s / max(one, 1e-6))))
+    t0 = time.perf_counter()
+    for i in range(reps):
+        ol.forward(xs[i % len(xs)][:T])
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(reps * T / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": (f"{reps} forwards of T={T} ({reps * T} tokens) of the same layer and routing, "
+                   f"C restatement of model/moe.go (gcc -O2 -ffp-contract=off), one call per token as "
+                   f"decodeLayers does; router/shared bf16 GEMVs on {threads} threads "
+                   f"(GOMAXPROCS-equivalent min(nproc,8)), expert GEMVs single-threaded; Go is not "
+                   f"installed on the box"),
+        "seconds": round(dt, 2),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              f"(the MoE block is built and measured on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    key, T, scope_kind, desc = WORKLOADS[args.workload]
+    cfg = qmoe.CONFIGS[key]
+    scope = cfg.n_experts if scope_kind == "E" else cfg.top_k
+    cfg = cfg.with_(select_scope=scope)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+
+    t_gen = time.perf_counter()
+    hw = qmoe.synthetic_weights(cfg, args.seed)
+    lb = qmoe.layer_bytes(cfg)
+    layer_total = lb["router"] + cfg.n_experts * lb["per_expert"] + lb["shared"]
+    step_bytes_est = lb["router"] + min(cfg.n_experts, T * cfg.top_k) * lb["per_expert"] + lb["shared"]
+    copies = args.copies or max(1, min(32, math.ceil(2 * 256e6 / step_bytes_est) + 1))
+    layers = []
+    for _ in range(copies):
+        L = qmoe.MoeLayer(cfg)
+        hw.upload(L)
+        layers.append(L)
+    gen_s = time.perf_counter() - t_gen
+
+    n_x = 64
+    xs_host = [qmoe.synthetic_tokens(cfg, T, args.seed + 1000 + i) for i in range(n_x)]
+    d_x = torch.from_numpy(np.stack(xs_host)).to(dev).contiguous()   # (n_x, T, H)
+    d_out = torch.empty((T, cfg.hidden), dtype=torch.float32, device=dev)
+    d_ids = torch.empty((n_x, T, cfg.top_k), dtype=torch.int32, device=dev)
+    d_w = torch.empty((n_x, T, cfg.top_k), dtype=torch.float32, device=dev)
+    xstride = T * cfg.hidden * 4
+    kstride = T * cfg.top_k * 4
+
+    def step(s, L=None):
+        i = s % n_x
+        (L or layers[s % copies]).forward_device(d_x.data_ptr() + i * xstride, T, d_out.data_ptr(),
+                                                 d_ids.data_ptr() + i * kstride, d_w.data_ptr() + i * kstride,
+                                                 sptr)
+
+    # routing of every x in the pool (same for every copy)
+    for i in range(n_x):
+        step(i, layers[0])
+    torch.cuda.synchronize()
+    ids_all = d_ids.cpu().numpy()
+    per_x_bytes = [stage_bytes(cfg, T, ids_all[i]) for i in range(n_x)]
+
+    # warmup, all stages profiled to find the dominant kernel
+    all_stages = [qmoe.STAGE_ROUTER, qmoe.STAGE_SELECT, qmoe.STAGE_GATE_UP, qmoe.STAGE_DOWN, qmoe.STAGE_FUSED]
+    for L in layers:
+        L.profile_enable(all_stages)
+        L.profile_read(reset=True)
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+    tot_ms = np.zeros(qmoe.STAGE_COUNT)
+    tot_n = np.zeros(qmoe.STAGE_COUNT, np.int64)
+    for L in layers:
+        ms, n = L.profile_read(reset=True)
+        tot_ms += ms
+        tot_n += n
+    stage_avg_us = {qmoe.STAGE_NAMES[s]: round(1e3 * tot_ms[s] / max(tot_n[s], 1), 3)
+                    for s in all_stages if tot_n[s]}
+    # dominant HBM-bound kernel: the one with the most time among the weight-streaming stages
+    weight_stages = [qmoe.STAGE_GATE_UP, qmoe.STAGE_DOWN, qmoe.STAGE_FUSED]
+    dom = max(weight_stages, key=lambda s: tot_ms[s])
+
+    # timed region: only the dominant kernel carries events
+    for L in layers:
+        L.profile_enable([dom])
+        L.profile_read(reset=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(s)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    dom_ms = 0.0
+    dom_n = 0
+    for L in layers:
+        ms, n = L.profile_read(reset=True)
+        dom_ms += ms[dom]
+        dom_n += int(n[dom])
+    dom_avg_s = dom_ms / 1e3 / max(dom_n, 1)
+    dom_bytes = float(np.mean([per_x_bytes[s % n_x][dom] for s in range(args.steps)]))
+    achieved = dom_bytes / dom_avg_s / 1e9
+
+    # whole-layer roofline: all algorithmic bytes / measured step time
+    def layer_step_bytes(bmap):
+        if tot_n[qmoe.STAGE_FUSED]:
+            return bmap[qmoe.STAGE_ROUTER] + bmap[qmoe.STAGE_FUSED]
+        return sum(v for st, v in bmap.items() if st != qmoe.STAGE_FUSED and tot_n[st])
+    layer_bytes_step = float(np.mean([layer_step_bytes(per_x_bytes[s % n_x]) for s in range(args.steps)]))
+    ms_per_step = 1e3 * elapsed / args.steps
+    layer_gbs = layer_bytes_step / (elapsed / args.steps) / 1e9
+
+    result = {
+        "metric": "MoE-layer tokens/s (decode T=1, prefill T=2048) + % of HBM/MFMA roofline",
+        "value": round(T * args.steps / elapsed, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": desc, "tokens_per_step": T, "hidden": cfg.hidden, "n_experts": cfg.n_experts,
+            "top_k": cfg.top_k, "moe_inter": cfg.moe_inter, "shared_inter": cfg.shared_inter,
+            "select_scope": scope, "router_fmt": qmoe.FORMAT_NAMES[cfg.router_fmt],
+            "expert_fmt": qmoe.FORMAT_NAMES[cfg.expert_fmt], "weight_copies": copies,
+            "weight_bytes_per_copy": layer_total, "x_pool": n_x, "seed": args.seed,
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": qmoe.STAGE_NAMES[dom], "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None, "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_avg_s * 1e6, 3),
+        },
+        "layer_roofline": {
+            "bytes_per_step": int(layer_bytes_step), "achieved_gbs": round(layer_gbs, 1),
+            "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "stage_avg_us": stage_avg_us,
+        },
+    }
+    if not args.no_cpu_baseline:
+        scope_for_oracle = scope
+        result["cpu_baseline"] = cpu_baseline(hw, cfg, T, scope_for_oracle, xs_host, args.cpu_seconds)
+    print(f"# setup {gen_s:.1f}s, {copies} copies x {layer_total / 1e9:.2f} GB", file=sys.stderr)
+    for L in layers:
+        L.close()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

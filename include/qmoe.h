@@ -130,6 +130,34 @@ qmoe_status qmoe_forward_device(qmoe_layer *layer, const float *d_x, int32_t T, 
  * expert is ignored for which >= 2.  out is a host array of rows*cols f32. */
 qmoe_status qmoe_dequant_debug(qmoe_layer *layer, int32_t which, int32_t expert, float *out);
 
+/* Kernel stages of one forward, for qmoe_profile_*. */
+enum {
+    QMOE_STAGE_ROUTER = 0,         /* router logits */
+    QMOE_STAGE_SELECT = 1,         /* softmax + selection + renormalisation */
+    QMOE_STAGE_GATE_UP = 2,        /* routed experts gate_up + SwiGLU */
+    QMOE_STAGE_SHARED_GATE_UP = 3, /* shared expert gate_up + SwiGLU + gate */
+    QMOE_STAGE_DOWN = 4,           /* down + weighted combine + shared */
+    QMOE_STAGE_FUSED = 5,          /* decode: routing + gate_up + down in one kernel */
+    QMOE_STAGE_COUNT = 8
+};
+
+/* Instrumentation with no reference counterpart (the reference has no
+ * timers): when bit s of stage_mask is set, every later forward records a HIP
+ * event pair on its stream around stage s's kernel launch.  qmoe_profile_read
+ * waits for the recorded events and returns the summed milliseconds and the
+ * launch count per stage (arrays of QMOE_STAGE_COUNT); reset != 0 zeroes the
+ * totals.  Events are released back to the handle's pool on each read, so read
+ * at least every few thousand forwards. */
+qmoe_status qmoe_profile_enable(qmoe_layer *layer, uint32_t stage_mask);
+qmoe_status qmoe_profile_read(qmoe_layer *layer, double *stage_ms, int64_t *stage_launches,
+                              int32_t reset);
+
+/* Diagnostics with no reference counterpart: the number of tokens, since
+ * qmoe_create, whose routing the certified decode router could not certify
+ * (a near or exact tie within its rounding bound) and therefore recomputed
+ * with the exact sequential path.  Synchronises the device. */
+qmoe_status qmoe_router_fallbacks(qmoe_layer *layer, int64_t *count);
+
 /* Bytes of device memory held by the handle (weights + workspace). */
 int64_t qmoe_device_bytes(const qmoe_layer *layer);
 

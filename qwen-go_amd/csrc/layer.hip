@@ -50,7 +50,21 @@ struct qmoe_layer {
   DevBuf ws;
   float *logits = nullptr, *wts = nullptr, *act = nullptr, *act_s = nullptr, *sg = nullptr;
   float *xbuf = nullptr, *obuf = nullptr;
+  double *sb = nullptr;
   int32_t *ids = nullptr;
+  unsigned int *fallbacks = nullptr;  // tokens routed by the exact fallback
+
+  // optional per-stage event timing (qmoe_profile_*)
+  uint32_t prof_mask = 0;
+  std::vector<hipEvent_t> ev_pool;
+  size_t ev_used = 0;
+  struct Rec {
+    int stage;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> recs;
+  double prof_ms[QMOE_STAGE_COUNT] = {};
+  int64_t prof_calls[QMOE_STAGE_COUNT] = {};
 };
 
 namespace {
@@ -105,6 +119,10 @@ qmoe_status alloc_mat(qmoe_layer *l, DevMat &m, int fmt, int64_t n_mat, int rows
 }
 
 void free_all(qmoe_layer *l) {
+  for (auto e : l->ev_pool) (void)hipEventDestroy(e);
+  l->ev_pool.clear();
+  l->recs.clear();
+  l->ev_used = 0;
   for (auto &b : l->owned)
     if (b.p) (void)hipFree(b.p);
   l->owned.clear();
@@ -132,6 +150,35 @@ qmoe_status enter(qmoe_layer *l) {
   return QMOE_OK;
 }
 
+hipError_t next_event(qmoe_layer *l, hipEvent_t *ev) {
+  if (l->ev_used == l->ev_pool.size()) {
+    hipEvent_t e;
+    hipError_t r = hipEventCreate(&e);
+    if (r != hipSuccess) return r;
+    l->ev_pool.push_back(e);
+  }
+  *ev = l->ev_pool[l->ev_used++];
+  return hipSuccess;
+}
+
+// Records an event pair around one kernel launch on its own stream when the
+// stage is selected by qmoe_profile_enable.
+#define STAGE(l, sid, st, expr, what)                                         \
+  do {                                                                        \
+    hipEvent_t _a = nullptr, _b = nullptr;                                    \
+    const bool _on = ((l)->prof_mask >> (sid)) & 1u;                          \
+    if (_on) {                                                                \
+      HIP_TRY(l, next_event(l, &_a), "hipEventCreate");                       \
+      HIP_TRY(l, next_event(l, &_b), "hipEventCreate");                       \
+      HIP_TRY(l, hipEventRecord(_a, st), "hipEventRecord");                   \
+    }                                                                         \
+    HIP_TRY(l, expr, what);                                                   \
+    if (_on) {                                                                \
+      HIP_TRY(l, hipEventRecord(_b, st), "hipEventRecord");                   \
+      (l)->recs.push_back({(sid), _a, _b});                                   \
+    }                                                                         \
+  } while (0)
+
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
@@ -148,6 +195,7 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_sg = take((size_t)nT * 4);
   size_t o_x = take((size_t)nT * d.hidden * 4);
   size_t o_o = take((size_t)nT * d.hidden * 4);
+  size_t o_sb = take((size_t)nT * d.n_experts * 16);
   // Pending work of earlier calls may still read the old workspace.
   if (user_stream) HIP_TRY(l, hipStreamSynchronize(user_stream), "hipStreamSynchronize");
   HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
@@ -169,6 +217,7 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   l->sg = (float *)(b + o_sg);
   l->xbuf = (float *)(b + o_x);
   l->obuf = (float *)(b + o_o);
+  l->sb = (double *)(b + o_sb);
   l->ws_T = nT;
   return QMOE_OK;
 }
@@ -182,8 +231,57 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   float *wts = d_w ? d_w : l->wts;
   const int H = d.hidden, E = d.n_experts, k = d.top_k, I = d.moe_inter, Is = d.shared_inter;
 
-  HIP_TRY(l, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
-  HIP_TRY(l, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st), "softmax/select launch");
+  const bool cert = T <= 32 && router_certified_supported(l->router);
+  if (cert && T <= kFusedMaxT && (Is == 0 || d.shared_fmt == d.expert_fmt)) {
+    // decode path: router partials (+ zero out), then one fused expert kernel
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, d_out, st), "router launch");
+    FusedArgs f{};
+    f.x = d_x;
+    f.T = T;
+    f.H = H;
+    f.E = E;
+    f.k = k;
+    f.scope = l->scope;
+    f.I = I;
+    f.Is = Is;
+    f.rw = l->router.w;
+    f.rs = l->router.s;
+    f.rfmt = l->router.fmt;
+    f.sb = l->sb;
+    f.fmt = l->gu.fmt;
+    f.gu = l->gu.w;
+    f.gu_s = l->gu.s;
+    f.gu_bytes = l->gu.mat_bytes;
+    f.gu_scales = l->gu.mat_scales;
+    f.dn = l->dn.w;
+    f.dn_s = l->dn.s;
+    f.dn_bytes = l->dn.mat_bytes;
+    f.dn_scales = l->dn.mat_scales;
+    if (Is > 0) {
+      f.sgate = l->sgate.w;
+      f.sup = l->sup.w;
+      f.sdown = l->sdown.w;
+      f.sgate_s = l->sgate.s;
+      f.sup_s = l->sup.s;
+      f.sdown_s = l->sdown.s;
+      f.shared_gate = l->shared_gate;
+    }
+    f.ids = ids;
+    f.weights = wts;
+    f.fallbacks = l->fallbacks;
+    f.out = d_out;
+    STAGE(l, QMOE_STAGE_FUSED, st, launch_expert_fused(f, st), "fused expert launch");
+    return QMOE_OK;
+  }
+  if (cert) {
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, nullptr, st), "router launch");
+    STAGE(l, QMOE_STAGE_SELECT, st,
+          launch_select_cert(d_x, T, l->router, k, l->scope, l->sb, ids, wts, l->fallbacks, st), "select launch");
+  } else {
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
+    STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st),
+          "softmax/select launch");
+  }
 
   GateUpArgs g{};
   g.x = d_x;
@@ -193,35 +291,23 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   g.H = H;
   g.I = I;
   g.gate = l->gu.w;
-  g.up = l->gu.w + fmt_matrix_bytes(l->gu.fmt, I, H);
   g.gate_s = l->gu.s;
-  g.up_s = l->gu.s ? l->gu.s + (int64_t)I * (H / kGroup) : nullptr;
   g.expert_bytes = l->gu.mat_bytes;
   g.expert_scales = l->gu.mat_scales;
   g.fmt = l->gu.fmt;
   g.act = l->act;
-  HIP_TRY(l, launch_gate_up_gemv(g, st), "gate_up launch");
-
+  g.Is = Is;
   if (Is > 0) {
-    GateUpArgs s{};
-    s.x = d_x;
-    s.ids = nullptr;
-    s.T = T;
-    s.k = 1;
-    s.H = H;
-    s.I = Is;
-    s.gate = l->sgate.w;
-    s.up = l->sup.w;
-    s.gate_s = l->sgate.s;
-    s.up_s = l->sup.s;
-    s.expert_bytes = 0;
-    s.expert_scales = 0;
-    s.fmt = l->sgate.fmt;
-    s.act = l->act_s;
-    s.shared_gate = l->shared_gate;
-    s.sg = l->sg;
-    HIP_TRY(l, launch_gate_up_gemv(s, st), "shared gate_up launch");
+    g.sgate = l->sgate.w;
+    g.sup = l->sup.w;
+    g.sgate_s = l->sgate.s;
+    g.sup_s = l->sup.s;
+    g.sfmt = l->sgate.fmt;
+    g.act_s = l->act_s;
+    g.shared_gate = l->shared_gate;
+    g.sg = l->sg;
   }
+  STAGE(l, QMOE_STAGE_GATE_UP, st, launch_gate_up_gemv(g, st), "gate_up launch");
 
   DownArgs a{};
   a.act = l->act;
@@ -243,7 +329,7 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   a.sdown_s = Is > 0 ? l->sdown.s : nullptr;
   a.sfmt = Is > 0 ? l->sdown.fmt : l->dn.fmt;
   a.out = d_out;
-  HIP_TRY(l, launch_down_gemv(a, st), "down launch");
+  STAGE(l, QMOE_STAGE_DOWN, st, launch_down_gemv(a, st), "down launch");
   return QMOE_OK;
 }
 
@@ -285,8 +371,8 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
     return fail(nullptr, QMOE_ERR_UNSUPPORTED, "n_experts > 1024 or top_k > 64");
   if (d.hidden > 16384)
     return fail(nullptr, QMOE_ERR_UNSUPPORTED, "hidden > 16384");
-  if ((int64_t)(d.top_k * d.moe_inter + d.shared_inter) * 4 > 64 * 1024)
-    return fail(nullptr, QMOE_ERR_UNSUPPORTED, "top_k * moe_inter + shared_inter exceeds 16384 floats");
+  if ((int64_t)(d.top_k + 1) * (std::max(d.moe_inter, d.shared_inter) + 8) * 4 > 64 * 1024)
+    return fail(nullptr, QMOE_ERR_UNSUPPORTED, "(top_k + 1) * max(moe_inter, shared_inter) exceeds 16K floats");
   int ndev = 0;
   hipError_t e = hipGetDeviceCount(&ndev);
   if (e != hipSuccess) return hip_fail(nullptr, e, "hipGetDeviceCount");
@@ -314,6 +400,18 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
     free_all(l);
     delete l;
     return s;
+  }
+  {
+    DevBuf b;
+    b.n = 256;
+    if (hipMalloc(&b.p, b.n) != hipSuccess || hipMemset(b.p, 0, b.n) != hipSuccess) {
+      (void)hipGetLastError();
+      free_all(l);
+      delete l;
+      return fail(nullptr, QMOE_ERR_NOMEM, "hipMalloc of the fallback counter failed");
+    }
+    l->owned.push_back(b);
+    l->fallbacks = (unsigned int *)b.p;
   }
   if (Is > 0) {
     DevBuf b;
@@ -497,6 +595,52 @@ qmoe_status qmoe_dequant_debug(qmoe_layer *l, int32_t which, int32_t expert, flo
   if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
   (void)hipFree(tmp);
   if (e != hipSuccess) return hip_fail(l, e, "dequant_debug");
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_profile_enable(qmoe_layer *l, uint32_t stage_mask) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  l->prof_mask = stage_mask & ((1u << QMOE_STAGE_COUNT) - 1u);
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_profile_read(qmoe_layer *l, double *stage_ms, int64_t *stage_launches, int32_t reset) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (!l->recs.empty()) HIP_TRY(l, hipEventSynchronize(l->recs.back().b), "hipEventSynchronize");
+  for (const auto &r : l->recs) {
+    float ms = 0.0f;
+    HIP_TRY(l, hipEventElapsedTime(&ms, r.a, r.b), "hipEventElapsedTime");
+    l->prof_ms[r.stage] += ms;
+    l->prof_calls[r.stage] += 1;
+  }
+  l->recs.clear();
+  l->ev_used = 0;
+  for (int i = 0; i < QMOE_STAGE_COUNT; i++) {
+    if (stage_ms) stage_ms[i] = l->prof_ms[i];
+    if (stage_launches) stage_launches[i] = l->prof_calls[i];
+    if (reset) {
+      l->prof_ms[i] = 0.0;
+      l->prof_calls[i] = 0;
+    }
+  }
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_router_fallbacks(qmoe_layer *l, int64_t *count) {
+  if (!l || !count) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  HIP_TRY(l, hipDeviceSynchronize(), "hipDeviceSynchronize");
+  unsigned int v = 0;
+  HIP_TRY(l, hipMemcpy(&v, l->fallbacks, sizeof(v), hipMemcpyDeviceToHost), "fallback counter read");
+  *count = v;
   return QMOE_OK;
 }
 

@@ -10,10 +10,13 @@
 // separately rounded, as Go on amd64 does.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "select.hpp"
 
 #include <math.h>
 
 namespace qmoe {
+
+constexpr int kMaxE = 1024;
 
 // Widens element k of a stored router row to f32 exactly as the reference:
 // bf16 -> bits << 16, int8 -> float(code) * scale, int4 -> float(nibble-8) * scale.
@@ -164,109 +167,186 @@ hipError_t launch_router_logits(const float *x, int T, const DevMat &router, flo
   }
 }
 
-// One wavefront per token.  softmax as model/tensors.go:106-121: max, then
-// v = float32(exp(float64(l - max))) summed sequentially in expert order, then
-// v / sum.  Selection (model/moe.go:44-53 generalised to the first `scope`
-// candidates): k rounds of a wavefront arg-max on (p descending, index
-// ascending), which is exactly the order of the reference's stable insertion
-// sort.  Renormalisation (moe.go:54-57, 63): wSum summed in rank order,
-// w = p / (wSum + 1e-9f).
-constexpr int kMaxE = 1024;
-constexpr int kMaxK = 64;
+// One wavefront per token: exact softmax + selection + renormalisation on
 
-__global__ void __launch_bounds__(64) softmax_select_kernel(const float *__restrict__ logits, int T,
-                                                            int E, int k, int scope,
-                                                            int32_t *__restrict__ ids,
+// One wavefront per token: exact softmax + selection + renormalisation on
+// the exact logits (select.hpp).
+template <int NJ>
+__global__ void __launch_bounds__(64) softmax_select_kernel(const float *__restrict__ logits, int E, int k,
+                                                            int scope, int32_t *__restrict__ ids,
                                                             float *__restrict__ weights) {
-#pragma clang fp contract(off)
-  __shared__ float buf[kMaxE];
-  __shared__ float selp[kMaxK];
-  __shared__ int seli[kMaxK];
-  __shared__ float ssum;
   const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  constexpr int NJ = kMaxE / 64;
-  const float *lt = logits + (size_t)t * E;
-  float v[NJ];
-  float mx = -INFINITY;
+  select_exact_nj<NJ>(logits + (size_t)t * E, E, k, scope, ids + (size_t)t * k, weights + (size_t)t * k, nullptr,
+                      nullptr);
+}
+
+hipError_t launch_softmax_select(const float *logits, int T, int E, int k, int scope, int32_t *ids,
+                                 float *weights, hipStream_t st) {
+#define L(NJ) hipLaunchKernelGGL(softmax_select_kernel<NJ>, dim3(T), dim3(64), 0, st, logits, E, k, scope, ids, weights)
+  QMOE_NJ_DISPATCH(E, L);
+#undef L
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Certified router for decode-sized T.
+//
+// The exact logits above cost one dependent f32 add per h per (token, expert)
+// -- about 2 instructions x H cycles of latency, several microseconds at
+// T = 1.  This path computes the same products p_h = fl(x_h * w_h) (identical
+// IEEE multiplies) and sums them in f64 across the wavefront, giving S ~ the
+// exact sum.  The reference's sequential f32 sum s_H differs from S by at most
+//   B = u (1 + 2 H u) sum_h |S_h|,   u = 2^-24, S_h the exact prefix sums
+// (each add rounds with relative error <= u; the f64 prefix sums come from a
+// wavefront scan).  Selection (select.hpp, certified_select_lds) then runs on
+// S and certifies every rank; a token that fails (a near tie, or an exact tie
+// that the index must break) is recomputed with the exact sequential logits.
+// Either way the ids are the reference's bit for bit.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ double seq_sum_bound(double babs, double pabs, int H) {
+  const double u = 0x1p-24;
+  return u * (1.0 + 2.0 * H * u + 1e-9) * babs + 1e-12 * pabs;
+}
+
+// One wavefront per (token, expert) writes sb[(t, e)] = {S, B}.  Block (0, t)
+// also zeroes out[t] when zero_out != nullptr (the fused expert kernel
+// accumulates into it).
+template <int FMT, int CPL>
+__global__ void __launch_bounds__(256) router_sb_kernel(const float *__restrict__ x, int H,
+                                                        const uint8_t *__restrict__ w,
+                                                        const uint16_t *__restrict__ s, int E,
+                                                        double *__restrict__ sb, float *__restrict__ zero_out) {
+#pragma clang fp contract(off)
+  constexpr int EPC = Chunk<FMT>::kElems;
+  constexpr int NP = CPL * EPC;  // products per lane
+  const int t = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + wave;
+  const int nch = H / EPC;
+  const float *xt = x + (size_t)t * H;
+  if (zero_out && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < H; i += 256) zero_out[(size_t)t * H + i] = 0.0f;
+  if (e >= E) return;
+  const uint8_t *row = w + (size_t)e * fmt_matrix_bytes(FMT, 1, H);
+  const uint16_t *srow = fmt_quant(FMT) ? s + (size_t)e * (H / kGroup) : nullptr;
+  float p[NP];
 #pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    int e = lane + 64 * j;
-    v[j] = e < E ? lt[e] : -INFINITY;
-    mx = fmaxf(mx, v[j]);
-  }
-  mx = wave_max(mx);
+  for (int c = 0; c < CPL; c++) {
+    const int ch = lane * CPL + c;
+    float wv[EPC];
+    if (ch < nch) {
+      router_chunk<FMT>(row, srow, ch, wv);
 #pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    int e = lane + 64 * j;
-    if (e < E) {
-      v[j] = (float)exp((double)(v[j] - mx));
-      buf[e] = v[j];
-    }
-  }
-  __syncthreads();
-  if (lane == 0) {
-    float sum = 0.0f;
-    for (int e = 0; e < E; e++) sum = sum + buf[e];
-    ssum = sum;
-  }
-  __syncthreads();
-  const float sum = ssum;
-  float key[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; j++) {
-    int e = lane + 64 * j;
-    float p = v[j] / sum;
-    v[j] = p;
-    // NaN ranks below every number so that k valid ids are always produced.
-    key[j] = (e < scope && p == p) ? p : -INFINITY;
-  }
-  uint32_t taken = 0;
-  for (int r = 0; r < k; r++) {
-    float bk = -INFINITY, bp = 0.0f;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-      int e = lane + 64 * j;
-      bool cand = e < scope && !((taken >> j) & 1u);
-      if (cand && (key[j] > bk || (key[j] == bk && e < bi))) {
-        bk = key[j];
-        bp = v[j];
-        bi = e;
+      for (int i = 0; i < EPC; i += 4) {
+        const float4 xv = *reinterpret_cast<const float4 *>(xt + ch * EPC + i);
+        p[c * EPC + i + 0] = xv.x * wv[i + 0];
+        p[c * EPC + i + 1] = xv.y * wv[i + 1];
+        p[c * EPC + i + 2] = xv.z * wv[i + 2];
+        p[c * EPC + i + 3] = xv.w * wv[i + 3];
       }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-      float ok = __shfl_xor(bk, o, 64);
-      float op = __shfl_xor(bp, o, 64);
-      int oi = __shfl_xor(bi, o, 64);
-      if (ok > bk || (ok == bk && oi < bi)) {
-        bk = ok;
-        bp = op;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    if (lane == 0) {
-      selp[r] = bp;
-      seli[r] = bi;
+    } else {
+#pragma unroll
+      for (int i = 0; i < EPC; i++) p[c * EPC + i] = 0.0f;
     }
   }
-  __syncthreads();
+  double tot = 0.0, pabs = 0.0;
+#pragma unroll
+  for (int i = 0; i < NP; i++) {
+    tot += (double)p[i];
+    pabs += fabs((double)p[i]);
+  }
+  const double inc = wave_incl_scan_f64(tot);  // lane totals -> exact prefix sums
+  double run = inc - tot, babs = 0.0;
+#pragma unroll
+  for (int i = 0; i < NP; i++) {
+    run += (double)p[i];
+    babs += fabs(run);
+  }
+  const double S = readlane_f64(inc, 63);
+  babs = wave_sum_f64(babs);
+  pabs = wave_sum_f64(pabs);
   if (lane == 0) {
-    float wsum = 0.0f;
-    for (int r = 0; r < k; r++) wsum = wsum + selp[r];
-    const float den = wsum + 1e-9f;
-    for (int r = 0; r < k; r++) {
-      ids[(size_t)t * k + r] = seli[r];
-      weights[(size_t)t * k + r] = selp[r] / den;
-    }
+    double *d = sb + ((size_t)t * E + e) * 2;
+    d[0] = S;
+    d[1] = seq_sum_bound(babs, pabs, H);
   }
 }
 
-hipError_t launch_softmax_select(const float *logits, int T, int E, int k, int scope,
-                                 int32_t *ids, float *weights, hipStream_t st) {
-  hipLaunchKernelGGL(softmax_select_kernel, dim3(T), dim3(64), 0, st, logits, T, E, k, scope, ids,
-                     weights);
+template <int FMT>
+static bool sb_fmt(const float *x, int T, const DevMat &r, double *sb, float *zero_out, hipStream_t st) {
+  constexpr int EPC = Chunk<FMT>::kElems;
+  const int H = r.cols, E = r.rows;
+  const int cpl = (H / EPC + 63) / 64;
+  dim3 grid((E + 3) / 4, T);
+#define L(C) hipLaunchKernelGGL((router_sb_kernel<FMT, C>), grid, dim3(256), 0, st, x, H, r.w, r.s, E, sb, zero_out)
+  // at most 64 products per lane (H <= 4096)
+  switch (cpl) {
+  case 1: L(1); return true;
+  case 2: if constexpr (2 * EPC <= 64) { L(2); return true; } return false;
+  case 4: if constexpr (4 * EPC <= 64) { L(4); return true; } return false;
+  case 8: if constexpr (8 * EPC <= 64) { L(8); return true; } return false;
+  default: return false;
+  }
+#undef L
+}
+
+bool router_certified_supported(const DevMat &router) {
+  const int epc = router.fmt == kF32 ? 4 : router.fmt == kBF16 ? 8 : router.fmt == kINT8 ? 16 : 32;
+  const int cpl = (router.cols / epc + 63) / 64;
+  return router.cols <= 4096 && router.rows <= kMaxE && (cpl == 1 || cpl == 2 || cpl == 4 || cpl == 8) &&
+         cpl * epc <= 64;
+}
+
+hipError_t launch_router_sb(const float *x, int T, const DevMat &router, double *sb, float *zero_out,
+                            hipStream_t st) {
+  switch (router.fmt) {
+  case kF32: sb_fmt<kF32>(x, T, router, sb, zero_out, st); break;
+  case kBF16: sb_fmt<kBF16>(x, T, router, sb, zero_out, st); break;
+  case kINT8: sb_fmt<kINT8>(x, T, router, sb, zero_out, st); break;
+  default: sb_fmt<kINT4>(x, T, router, sb, zero_out, st); break;
+  }
+  return hipGetLastError();
+}
+
+// One block per token: certified selection from S/B; on failure the block
+// computes the exact logits and selects on them.
+template <int NJ>
+__global__ void __launch_bounds__(256) select_cert_kernel(const float *__restrict__ x, DevMat router, int k,
+                                                          int scope, const double *__restrict__ sb,
+                                                          int32_t *__restrict__ ids, float *__restrict__ weights,
+                                                          unsigned int *__restrict__ fallbacks) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int ok;
+  const int t = blockIdx.x;
+  const int E = router.rows, H = router.cols;
+  float *xs = reinterpret_cast<float *>(smem);
+  float *lt = xs + H;
+  if (threadIdx.x < 64) {
+    const bool c = certified_select_nj<NJ>(sb + (size_t)t * E * 2, E, k, scope, ids + (size_t)t * k,
+                                           weights + (size_t)t * k, nullptr, nullptr);
+    if (threadIdx.x == 0) ok = c;
+  }
+  __syncthreads();
+  if (ok) return;
+  for (int i = threadIdx.x; i < H; i += 256) xs[i] = x[(size_t)t * H + i];
+  __syncthreads();
+  exact_logits_block(xs, H, router.w, router.s, router.fmt, E, lt);
+  __syncthreads();
+  if (threadIdx.x < 64)
+    select_exact_nj<NJ>(lt, E, k, scope, ids + (size_t)t * k, weights + (size_t)t * k, nullptr, nullptr);
+  if (threadIdx.x == 0) atomicAdd(fallbacks, 1u);
+}
+
+size_t select_cert_lds_bytes(int E, int H) { return (size_t)H * 4 + (size_t)E * 4; }
+
+hipError_t launch_select_cert(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
+                              int32_t *ids, float *weights, unsigned int *fallbacks, hipStream_t st) {
+  const size_t lds = select_cert_lds_bytes(router.rows, router.cols);
+#define L(NJ) hipLaunchKernelGGL(select_cert_kernel<NJ>, dim3(T), dim3(256), lds, st, x, router, k, scope, sb, ids, \
+                               weights, fallbacks)
+  QMOE_NJ_DISPATCH(router.rows, L);
+#undef L
   return hipGetLastError();
 }
 

@@ -66,6 +66,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_forward_device": ([vp, vp, i32, vp, vp, vp, vp], i32),
         "qmoe_dequant_debug": ([vp, i32, i32, vp], i32),
         "qmoe_device_bytes": ([vp], i64),
+        "qmoe_profile_enable": ([vp, ctypes.c_uint32], i32),
+        "qmoe_profile_read": ([vp, vp, vp, i32], i32),
+        "qmoe_router_fallbacks": ([vp, vp], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -79,7 +82,14 @@ def exported_symbols() -> list[str]:
     return ["qmoe_create", "qmoe_destroy", "qmoe_last_error", "qmoe_status_string",
             "qmoe_set_router", "qmoe_set_experts", "qmoe_set_shared", "qmoe_quantize_experts",
             "qmoe_quantize_device", "qmoe_forward", "qmoe_forward_device", "qmoe_dequant_debug",
-            "qmoe_device_bytes"]
+            "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks"]
+
+
+STAGE_ROUTER, STAGE_SELECT, STAGE_GATE_UP, STAGE_SHARED_GATE_UP, STAGE_DOWN, STAGE_FUSED = range(6)
+STAGE_COUNT = 8
+STAGE_NAMES = {STAGE_ROUTER: "router_logits", STAGE_SELECT: "softmax_select",
+               STAGE_GATE_UP: "gate_up", STAGE_SHARED_GATE_UP: "shared_gate_up", STAGE_DOWN: "down",
+               STAGE_FUSED: "fused_experts"}
 
 
 def _ptr(a):
@@ -199,6 +209,24 @@ class MoeLayer:
         self._check(self.lib.qmoe_dequant_debug(self.h, which, expert, _ptr(out)))
         return out
 
+    def profile_enable(self, stages) -> None:
+        mask = 0
+        for st in stages:
+            mask |= 1 << st
+        self._check(self.lib.qmoe_profile_enable(self.h, mask))
+
+    def profile_read(self, reset: bool = True):
+        """-> (ms per stage, launches per stage), summed since the last reset."""
+        ms = np.zeros(STAGE_COUNT, np.float64)
+        n = np.zeros(STAGE_COUNT, np.int64)
+        self._check(self.lib.qmoe_profile_read(self.h, _ptr(ms), _ptr(n), 1 if reset else 0))
+        return ms, n
+
+    def router_fallbacks(self) -> int:
+        n = ctypes.c_int64()
+        self._check(self.lib.qmoe_router_fallbacks(self.h, ctypes.byref(n)))
+        return int(n.value)
+
     def device_bytes(self) -> int:
         return int(self.lib.qmoe_device_bytes(self.h))
 
@@ -265,8 +293,30 @@ def algorithmic_flops(cfg: LayerConfig, T: int) -> int:
     return T * f
 
 
-def _normal(rng: np.random.Generator, shape, std: float) -> np.ndarray:
-    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+_BIG = 1 << 24  # elements; larger arrays come from torch's multi-threaded CPU generator
+
+
+def _normal(seed: int, shape, std: float) -> np.ndarray:
+    """float32 ~ N(0, std^2) from a seed.  Small arrays use numpy's PCG64
+    (identical on every machine with the same numpy); large ones use a seeded
+    torch CPU generator for speed.  Either way both the device and the oracle
+    consume the same host array."""
+    n = int(np.prod(shape))
+    if n <= _BIG:
+        rng = np.random.default_rng(seed)
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    t = torch.randn(tuple(shape), generator=g, dtype=torch.float32)
+    t.mul_(std)
+    return t.numpy()
+
+
+def _to_bf16(w: np.ndarray) -> np.ndarray:
+    if w.size <= _BIG:
+        return f32_to_bf16_bits(w)
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(w, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
 
 
 @dataclass
@@ -301,7 +351,7 @@ def _store(fmt: int, w: np.ndarray, n_mat: int, rows: int, cols: int, quantizer)
     if fmt == F32:
         return np.ascontiguousarray(w, np.float32), None
     if fmt == BF16:
-        return f32_to_bf16_bits(w), None
+        return _to_bf16(w), None
     return quantizer(8 if fmt == INT8G32 else 4, w, n_mat, rows, cols)
 
 
@@ -326,25 +376,25 @@ def synthetic_weights(cfg: LayerConfig, seed: int, quantizer=device_quantizer,
                       router_scale: float = 1.0) -> HostWeights:
     """Seeded N(0, 0.02) weights in cfg's formats.  router_scale multiplies the
     router weights before rounding (x4 sharpens the logits)."""
-    rng = np.random.default_rng(seed)
     H, E, I, Is = cfg.hidden, cfg.n_experts, cfg.moe_inter, cfg.shared_inter
-    r32 = _normal(rng, (E, H), 0.02) * np.float32(router_scale)
+    s0 = seed * 1000
+    r32 = _normal(s0 + 1, (E, H), 0.02) * np.float32(router_scale)
     router, router_s = _store(cfg.router_fmt, r32, 1, E, H, quantizer)
-    gu32 = _normal(rng, (E, 2 * I, H), 0.02)
+    gu32 = _normal(s0 + 2, (E, 2 * I, H), 0.02)
     gate_up, gate_up_s = _store(cfg.expert_fmt, gu32, E, 2 * I, H, quantizer)
     del gu32
-    dn32 = _normal(rng, (E, H, I), 0.02)
+    dn32 = _normal(s0 + 3, (E, H, I), 0.02)
     down, down_s = _store(cfg.expert_fmt, dn32, E, H, I, quantizer)
     del dn32
     hw = HostWeights(cfg, router, router_s, gate_up, gate_up_s, down, down_s)
     if Is:
-        g = _normal(rng, (Is, H), 0.02)
-        u = _normal(rng, (Is, H), 0.02)
-        dd = _normal(rng, (H, Is), 0.02)
+        g = _normal(s0 + 4, (Is, H), 0.02)
+        u = _normal(s0 + 5, (Is, H), 0.02)
+        dd = _normal(s0 + 6, (H, Is), 0.02)
         hw.sh_gate, hw.sh_gate_s = _store(cfg.shared_fmt, g, 1, Is, H, quantizer)
         hw.sh_up, hw.sh_up_s = _store(cfg.shared_fmt, u, 1, Is, H, quantizer)
         hw.sh_down, hw.sh_down_s = _store(cfg.shared_fmt, dd, 1, H, Is, quantizer)
-        hw.shared_gate = _normal(rng, (H,), 0.02)
+        hw.shared_gate = _normal(s0 + 7, (H,), 0.02)
     return hw
 
 

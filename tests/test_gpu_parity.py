@@ -3,7 +3,9 @@
 Bars (written into each assertion):
   * expert ids: exact, in rank order (the router sums each logit sequentially
     in f32 exactly as model/moe.go does);
-  * routing weights: exact up to the last bit of exp (tolerance 1e-6 relative);
+  * routing weights: 1e-4 relative (decode-sized T uses the certified router,
+    whose weights come from f64 logits within its rounding bound of the
+    reference's f32 logits; the exact path matches to the last bit of exp);
   * dequantised weights and device-quantised codes/scales: bit-exact;
   * layer output on the GEMV path (f32 activations): normwise relative error
     max_j|y-y_ref| / max_j|y_ref| <= 1e-3 per token.
@@ -37,7 +39,7 @@ def check_layer(cfg, hw, x, tol=TOL_F32, scope=None):
         layer.close()
     ref, rids, rw = oracle.OracleLayer(hw, scope=scope).forward(x)
     assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
-    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
+    np.testing.assert_allclose(w, rw, rtol=1e-4, atol=0)
     err = rel_err(out, ref)
     assert err <= tol, f"normwise relative error {err:.3e} > {tol}"
     return err
@@ -130,8 +132,11 @@ SMALL = [
 
 
 @pytest.mark.parametrize("fmts", SMALL, ids=lambda f: "-".join(map(str, f)))
-@pytest.mark.parametrize("T", [1, 3, 37])
+@pytest.mark.parametrize("T", [1, 3, 16, 37])
 def test_small_layers(fmts, T):
+    """T <= 8: certified router + fused expert kernel (same shared format) or
+    the separate kernels; 9..32: certified router + select + GEMVs; > 32:
+    exact tiled router + GEMVs."""
     rf, ef, sf, Is, scope = fmts
     cfg = qmoe.LayerConfig(320, 16, 4, 160, Is, scope, rf, ef, sf, "small")
     announce(f"small layer fmts={fmts} T={T}")
@@ -175,6 +180,39 @@ def test_qwen3_next_int4_decode():
     hw = qmoe.synthetic_weights(cfg, 99, quantizer=qmoe.device_quantizer)
     x = qmoe.synthetic_tokens(cfg, 2, 99)
     check_layer(cfg, hw, x)
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_router_exact_ties(T):
+    """Identical router rows give exactly equal logits; the reference breaks the
+    tie by the lower expert index.  The certified path cannot certify such a
+    gap and must fall back to the exact sequential path in-kernel."""
+    cfg = qmoe.LayerConfig(256, 16, 4, 64, 0, 16, qmoe.BF16, qmoe.BF16, qmoe.BF16, "ties")
+    announce(f"router exact ties T={T}")
+    hw = qmoe.synthetic_weights(cfg, 31, quantizer=oracle.host_quantizer)
+    r = hw.router.copy()
+    r[5] = r[3]           # 3 and 5 tie, 3 must rank first
+    r[9] = r[12] = r[2]   # three-way tie 2 < 9 < 12
+    hw.router = r
+    x = qmoe.synthetic_tokens(cfg, T, 31)
+    # make the tied experts win: align x with their rows
+    w3 = qmoe.bf16_bits_to_f32(r[3]).astype(np.float32)
+    w2 = qmoe.bf16_bits_to_f32(r[2]).astype(np.float32)
+    x = (x + 40.0 * w3 + 38.0 * w2).astype(np.float32)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(x)
+        fb = layer.router_fallbacks()
+    finally:
+        layer.close()
+    ref, rids, rw = oracle.OracleLayer(hw).forward(x)
+    assert np.array_equal(ids, rids), (ids, rids)
+    # the leading ranks are a tied group, listed in ascending index order
+    assert list(ids[0][:2]) in ([3, 5], [2, 9]), ids[0]
+    assert rel_err(out, ref) <= TOL_F32
+    if T <= 32:
+        assert fb >= T  # every token hit a tie
 
 
 # ----------------------------------------------------------- contract
