@@ -1,5 +1,5 @@
-// gemv_common.hpp -- device helpers of the bandwidth-bound expert GEMVs
-// (gate_up.hip, down.hip).
+// gemv_common.hpp -- device helpers of the bandwidth-bound expert products
+// (fused.hip): 16-byte weight chunks dotted with f32 activations in LDS.
 #pragma once
 
 #include "common.hpp"
@@ -10,7 +10,6 @@
 namespace qmoe {
 
 constexpr int kBlock = 256;
-constexpr int kDownRows = 8;  // output rows per down block
 
 // Largest power of two <= 64 that divides n (lanes per row).
 __host__ __device__ inline int lanes_per_row(int n) {
@@ -121,11 +120,6 @@ inline int iter_of(int fmt, int cols) {
   const int nch = cols / epc;
   const int it = nch / lanes_per_row(nch);
   return (it == 1 || it == 2 || it == 3 || it == 4 || it == 8) ? it : 0;
-}
-
-inline int rows_per_block_of(int fmt, int cols) {
-  const int epc = fmt == kF32 ? 4 : fmt == kBF16 ? 8 : fmt == kINT8 ? 16 : 32;
-  return (kBlock / 64) * (64 / lanes_per_row(cols / epc));
 }
 
 // Dispatch helper: the compile-time chunk counts that realistic shapes use.

@@ -2,13 +2,19 @@
 // forward orchestration of the MoE block on one gfx950 device.
 //
 // Forward (model/moe.go:41-99 for T tokens at once):
-//   1. router logits, exact sequential f32 per (token, expert)   router.hip
-//   2. softmax + selection over the first C + renormalisation     router.hip
-//   3. expert gate_up GEMV + SwiGLU (+ shared expert gate_up and
-//      its sigmoid gate)                                          gemv.hip
-//   4. expert down GEMV + weighted combine in rank order + shared  gemv.hip
+//   1. router: certified partials S/B per (token, expert) for T <= 32 (which
+//      also zero out), else the exact sequential logits + softmax/selection
+//      (router.hip)
+//   2. experts: one fused kernel -- routing, gate_up + SwiGLU, transposed down
+//      rows, f32 atomics into out (fused.hip); a shared expert stored in
+//      another format gets a second launch of the same kernel
 // All kernels run on one stream; the host-pointer entry copies x in and out
 // around them and synchronises, as the cgo seam needs.
+//
+// Device layouts: router and gate_up as in the reference (rows along H); the
+// down matrices (routed and shared) are stored transposed, (I, H) per expert,
+// so that a block's 32 intermediate rows are one contiguous region.  Codes and
+// scales are moved, never recomputed, so dequantisation stays bit-exact.
 #include "../../include/qmoe.h"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -48,7 +54,7 @@ struct qmoe_layer {
   // workspace, sized for ws_T tokens
   int ws_T = 0;
   DevBuf ws;
-  float *logits = nullptr, *wts = nullptr, *act = nullptr, *act_s = nullptr, *sg = nullptr;
+  float *logits = nullptr, *wts = nullptr;
   float *xbuf = nullptr, *obuf = nullptr;
   double *sb = nullptr;
   int32_t *ids = nullptr;
@@ -88,10 +94,12 @@ qmoe_status hip_fail(qmoe_layer *l, hipError_t e, const char *what) {
 bool valid_fmt(int f) { return f >= QMOE_F32 && f <= QMOE_INT4G32; }
 
 // Allocates a (n_mat x rows x cols) stack in fmt plus its scales.
-qmoe_status alloc_mat(qmoe_layer *l, DevMat &m, int fmt, int64_t n_mat, int rows, int cols) {
+qmoe_status alloc_mat(qmoe_layer *l, DevMat &m, int fmt, int64_t n_mat, int rows, int cols,
+                      bool transposed = false) {
   m.fmt = fmt;
   m.rows = rows;
   m.cols = cols;
+  m.transposed = transposed;
   m.mat_bytes = fmt_matrix_bytes(fmt, rows, cols);
   m.mat_scales = fmt_quant(fmt) ? (int64_t)rows * (cols / kGroup) : 0;
   DevBuf b;
@@ -133,9 +141,51 @@ void free_all(qmoe_layer *l) {
   l->stream = nullptr;
 }
 
+// Moves n stored matrices in the reference layout from device staging into
+// m (at matrix index first), transposing when m is stored transposed.
+qmoe_status place(qmoe_layer *l, const DevMat &m, int64_t first, int64_t n, const uint8_t *src, const uint16_t *ss) {
+  uint8_t *dst = (uint8_t *)m.w + first * m.mat_bytes;
+  uint16_t *ds = m.s ? (uint16_t *)m.s + first * m.mat_scales : nullptr;
+  if (m.transposed) {
+    HIP_TRY(l, launch_relayout_transpose(m.fmt, src, ss, n, m.rows, m.cols, dst, ds, l->stream), "relayout launch");
+  } else {
+    HIP_TRY(l, hipMemcpyAsync(dst, src, (size_t)(m.mat_bytes * n), hipMemcpyDeviceToDevice, l->stream), "copy");
+    if (ds)
+      HIP_TRY(l, hipMemcpyAsync(ds, ss, (size_t)(m.mat_scales * n) * 2, hipMemcpyDeviceToDevice, l->stream), "copy");
+  }
+  HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+  return QMOE_OK;
+}
+
 qmoe_status upload(qmoe_layer *l, const DevMat &m, int64_t n_mat, const void *w, const uint16_t *s) {
   if (!w) return fail(l, QMOE_ERR_INVALID, "null weight pointer");
   if (fmt_quant(m.fmt) && !s) return fail(l, QMOE_ERR_INVALID, "null scale pointer for a quantised format");
+  if (m.transposed) {
+    // stage at most ~256 MiB of the reference layout at a time
+    const int64_t per = m.mat_bytes + m.mat_scales * 2;
+    const int64_t chunk = std::min<int64_t>(n_mat, std::max<int64_t>(1, (256ll << 20) / per));
+    uint8_t *tmp = nullptr;
+    HIP_TRY(l, hipMalloc(&tmp, (size_t)(chunk * per)), "hipMalloc upload staging");
+    uint16_t *tsc = m.mat_scales ? (uint16_t *)(tmp + chunk * m.mat_bytes) : nullptr;
+    for (int64_t e0 = 0; e0 < n_mat; e0 += chunk) {
+      const int64_t n = std::min(chunk, n_mat - e0);
+      hipError_t e = hipMemcpy(tmp, (const uint8_t *)w + e0 * m.mat_bytes, (size_t)(n * m.mat_bytes),
+                               hipMemcpyHostToDevice);
+      if (e == hipSuccess && tsc)
+        e = hipMemcpy(tsc, s + e0 * m.mat_scales, (size_t)(n * m.mat_scales) * 2, hipMemcpyHostToDevice);
+      if (e != hipSuccess) {
+        (void)hipFree(tmp);
+        return hip_fail(l, e, "weight upload");
+      }
+      qmoe_status st = place(l, m, e0, n, tmp, tsc);
+      if (st != QMOE_OK) {
+        (void)hipFree(tmp);
+        return st;
+      }
+    }
+    (void)hipFree(tmp);
+    return QMOE_OK;
+  }
   HIP_TRY(l, hipMemcpy((void *)m.w, w, (size_t)(m.mat_bytes * n_mat), hipMemcpyHostToDevice), "weight upload");
   if (fmt_quant(m.fmt))
     HIP_TRY(l, hipMemcpy((void *)m.s, s, (size_t)(m.mat_scales * n_mat) * sizeof(uint16_t), hipMemcpyHostToDevice),
@@ -190,9 +240,6 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_logits = take((size_t)nT * d.n_experts * 4);
   size_t o_ids = take((size_t)nT * d.top_k * 4);
   size_t o_wts = take((size_t)nT * d.top_k * 4);
-  size_t o_act = take((size_t)nT * d.top_k * d.moe_inter * 4);
-  size_t o_acts = take((size_t)nT * std::max(d.shared_inter, 1) * 4);
-  size_t o_sg = take((size_t)nT * 4);
   size_t o_x = take((size_t)nT * d.hidden * 4);
   size_t o_o = take((size_t)nT * d.hidden * 4);
   size_t o_sb = take((size_t)nT * d.n_experts * 16);
@@ -212,9 +259,6 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   l->logits = (float *)(b + o_logits);
   l->ids = (int32_t *)(b + o_ids);
   l->wts = (float *)(b + o_wts);
-  l->act = (float *)(b + o_act);
-  l->act_s = (float *)(b + o_acts);
-  l->sg = (float *)(b + o_sg);
   l->xbuf = (float *)(b + o_x);
   l->obuf = (float *)(b + o_o);
   l->sb = (double *)(b + o_sb);
@@ -232,104 +276,59 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   const int H = d.hidden, E = d.n_experts, k = d.top_k, I = d.moe_inter, Is = d.shared_inter;
 
   const bool cert = T <= 32 && router_certified_supported(l->router);
-  if (cert && T <= kFusedMaxT && (Is == 0 || d.shared_fmt == d.expert_fmt)) {
-    // decode path: router partials (+ zero out), then one fused expert kernel
-    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, d_out, st), "router launch");
-    FusedArgs f{};
-    f.x = d_x;
-    f.T = T;
-    f.H = H;
-    f.E = E;
-    f.k = k;
-    f.scope = l->scope;
-    f.I = I;
-    f.Is = Is;
-    f.rw = l->router.w;
-    f.rs = l->router.s;
-    f.rfmt = l->router.fmt;
-    f.sb = l->sb;
-    f.fmt = l->gu.fmt;
-    f.gu = l->gu.w;
-    f.gu_s = l->gu.s;
-    f.gu_bytes = l->gu.mat_bytes;
-    f.gu_scales = l->gu.mat_scales;
-    f.dn = l->dn.w;
-    f.dn_s = l->dn.s;
-    f.dn_bytes = l->dn.mat_bytes;
-    f.dn_scales = l->dn.mat_scales;
-    if (Is > 0) {
-      f.sgate = l->sgate.w;
-      f.sup = l->sup.w;
-      f.sdown = l->sdown.w;
-      f.sgate_s = l->sgate.s;
-      f.sup_s = l->sup.s;
-      f.sdown_s = l->sdown.s;
-      f.shared_gate = l->shared_gate;
-    }
-    f.ids = ids;
-    f.weights = wts;
-    f.fallbacks = l->fallbacks;
-    f.out = d_out;
-    STAGE(l, QMOE_STAGE_FUSED, st, launch_expert_fused(f, st), "fused expert launch");
-    return QMOE_OK;
-  }
   if (cert) {
-    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, nullptr, st), "router launch");
-    STAGE(l, QMOE_STAGE_SELECT, st,
-          launch_select_cert(d_x, T, l->router, k, l->scope, l->sb, ids, wts, l->fallbacks, st), "select launch");
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, d_out, st), "router launch");
   } else {
     STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
     STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st),
           "softmax/select launch");
+    HIP_TRY(l, launch_zero(d_out, (int64_t)T * H, st), "zero launch");
   }
-
-  GateUpArgs g{};
-  g.x = d_x;
-  g.ids = ids;
-  g.T = T;
-  g.k = k;
-  g.H = H;
-  g.I = I;
-  g.gate = l->gu.w;
-  g.gate_s = l->gu.s;
-  g.expert_bytes = l->gu.mat_bytes;
-  g.expert_scales = l->gu.mat_scales;
-  g.fmt = l->gu.fmt;
-  g.act = l->act;
-  g.Is = Is;
+  FusedArgs f{};
+  f.x = d_x;
+  f.T = T;
+  f.H = H;
+  f.E = E;
+  f.k = k;
+  f.scope = l->scope;
+  f.I = I;
+  f.Is = Is;
+  f.rw = l->router.w;
+  f.rs = l->router.s;
+  f.rfmt = l->router.fmt;
+  f.sb = cert ? l->sb : nullptr;
+  f.fmt = l->gu.fmt;
+  f.gu = l->gu.w;
+  f.gu_s = l->gu.s;
+  f.gu_bytes = l->gu.mat_bytes;
+  f.gu_scales = l->gu.mat_scales;
+  f.dn = l->dn.w;
+  f.dn_s = l->dn.s;
+  f.dn_bytes = l->dn.mat_bytes;
+  f.dn_scales = l->dn.mat_scales;
   if (Is > 0) {
-    g.sgate = l->sgate.w;
-    g.sup = l->sup.w;
-    g.sgate_s = l->sgate.s;
-    g.sup_s = l->sup.s;
-    g.sfmt = l->sgate.fmt;
-    g.act_s = l->act_s;
-    g.shared_gate = l->shared_gate;
-    g.sg = l->sg;
+    f.sgate = l->sgate.w;
+    f.sup = l->sup.w;
+    f.sdown = l->sdown.w;
+    f.sgate_s = l->sgate.s;
+    f.sup_s = l->sup.s;
+    f.sdown_s = l->sdown.s;
+    f.shared_gate = l->shared_gate;
   }
-  STAGE(l, QMOE_STAGE_GATE_UP, st, launch_gate_up_gemv(g, st), "gate_up launch");
-
-  DownArgs a{};
-  a.act = l->act;
-  a.ids = ids;
-  a.weights = wts;
-  a.T = T;
-  a.k = k;
-  a.H = H;
-  a.I = I;
-  a.down = l->dn.w;
-  a.down_s = l->dn.s;
-  a.expert_bytes = l->dn.mat_bytes;
-  a.expert_scales = l->dn.mat_scales;
-  a.fmt = l->dn.fmt;
-  a.act_s = l->act_s;
-  a.sg = l->sg;
-  a.Is = Is;
-  a.sdown = Is > 0 ? l->sdown.w : nullptr;
-  a.sdown_s = Is > 0 ? l->sdown.s : nullptr;
-  a.sfmt = Is > 0 ? l->sdown.fmt : l->dn.fmt;
-  a.out = d_out;
-  STAGE(l, QMOE_STAGE_DOWN, st, launch_down_gemv(a, st), "down launch");
+  f.ids = ids;
+  f.weights = wts;
+  f.fallbacks = l->fallbacks;
+  f.out = d_out;
+  f.k_routed = k;
+  f.with_shared = Is > 0 && d.shared_fmt == d.expert_fmt;
+  STAGE(l, QMOE_STAGE_FUSED, st, launch_expert_fused(f, st), "fused expert launch");
+  if (Is > 0 && d.shared_fmt != d.expert_fmt) {
+    // shared expert in its own format: a second launch of the same kernel
+    f.fmt = d.shared_fmt;
+    f.k_routed = 0;
+    f.with_shared = 1;
+    STAGE(l, QMOE_STAGE_FUSED, st, launch_expert_fused(f, st), "fused shared-expert launch");
+  }
   return QMOE_OK;
 }
 
@@ -371,8 +370,9 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
     return fail(nullptr, QMOE_ERR_UNSUPPORTED, "n_experts > 1024 or top_k > 64");
   if (d.hidden > 16384)
     return fail(nullptr, QMOE_ERR_UNSUPPORTED, "hidden > 16384");
-  if ((int64_t)(d.top_k + 1) * (std::max(d.moe_inter, d.shared_inter) + 8) * 4 > 64 * 1024)
-    return fail(nullptr, QMOE_ERR_UNSUPPORTED, "(top_k + 1) * max(moe_inter, shared_inter) exceeds 16K floats");
+  if (!fused_supported(d.expert_fmt, d.hidden, d.n_experts) ||
+      (d.shared_inter > 0 && !fused_supported(d.shared_fmt, d.hidden, d.n_experts)))
+    return fail(nullptr, QMOE_ERR_UNSUPPORTED, "hidden too large for the expert kernel's LDS plan");
   int ndev = 0;
   hipError_t e = hipGetDeviceCount(&ndev);
   if (e != hipSuccess) return hip_fail(nullptr, e, "hipGetDeviceCount");
@@ -392,10 +392,10 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
   const int H = d.hidden, E = d.n_experts, I = d.moe_inter, Is = d.shared_inter;
   if ((s = alloc_mat(l, l->router, d.router_fmt, 1, E, H)) != QMOE_OK ||
       (s = alloc_mat(l, l->gu, d.expert_fmt, E, 2 * I, H)) != QMOE_OK ||
-      (s = alloc_mat(l, l->dn, d.expert_fmt, E, H, I)) != QMOE_OK ||
+      (s = alloc_mat(l, l->dn, d.expert_fmt, E, H, I, true)) != QMOE_OK ||
       (Is > 0 && ((s = alloc_mat(l, l->sgate, d.shared_fmt, 1, Is, H)) != QMOE_OK ||
                   (s = alloc_mat(l, l->sup, d.shared_fmt, 1, Is, H)) != QMOE_OK ||
-                  (s = alloc_mat(l, l->sdown, d.shared_fmt, 1, H, Is)) != QMOE_OK))) {
+                  (s = alloc_mat(l, l->sdown, d.shared_fmt, 1, H, Is, true)) != QMOE_OK))) {
     g_create_error = l->err;
     free_all(l);
     delete l;
@@ -512,17 +512,22 @@ qmoe_status qmoe_quantize_experts(qmoe_layer *l, const float *gate_up, const flo
     int64_t chunk = std::max<int64_t>(1, (256ll << 20) / (per * 4));
     chunk = std::min<int64_t>(chunk, E);
     float *tmp = nullptr;
-    HIP_TRY(l, hipMalloc(&tmp, (size_t)(chunk * per * 4)), "hipMalloc quantiser staging");
+    HIP_TRY(l, hipMalloc(&tmp, (size_t)(chunk * (per * 4 + m.mat_bytes + m.mat_scales * 2))),
+            "hipMalloc quantiser staging");
+    uint8_t *qc = (uint8_t *)(tmp + chunk * per);
+    uint16_t *qs = (uint16_t *)(qc + chunk * m.mat_bytes);
     for (int64_t e0 = 0; e0 < E; e0 += chunk) {
       int64_t n = std::min<int64_t>(chunk, E - e0);
       hipError_t err = hipMemcpy(tmp, src + e0 * per, (size_t)(n * per * 4), hipMemcpyHostToDevice);
-      if (err == hipSuccess)
-        err = launch_quantize(bits, tmp, n * m.rows, m.cols, (uint8_t *)m.w + e0 * m.mat_bytes,
-                              (uint16_t *)m.s + e0 * m.mat_scales, l->stream);
-      if (err == hipSuccess) err = hipStreamSynchronize(l->stream);
+      if (err == hipSuccess) err = launch_quantize(bits, tmp, n * m.rows, m.cols, qc, qs, l->stream);
       if (err != hipSuccess) {
         (void)hipFree(tmp);
         return hip_fail(l, err, "expert quantisation");
+      }
+      qmoe_status st = place(l, m, e0, n, qc, qs);
+      if (st != QMOE_OK) {
+        (void)hipFree(tmp);
+        return st;
       }
     }
     (void)hipFree(tmp);

@@ -88,26 +88,56 @@ hipError_t launch_quantize(int bits, const float *w, int64_t n_rows, int cols, u
   return hipGetLastError();
 }
 
+// Element (row o, column c) of a stored (rows, cols) matrix as f32, exactly as
+// quantLinear.dequantize / bf16f32 give it.
+template <int FMT>
+__device__ __forceinline__ float stored_value(const uint8_t *__restrict__ wq, const uint16_t *__restrict__ s,
+                                              int64_t o, int c, int cols) {
+#pragma clang fp contract(off)
+  if constexpr (FMT == kF32) {
+    return reinterpret_cast<const float *>(wq)[o * cols + c];
+  } else if constexpr (FMT == kBF16) {
+    return bf16_to_f32(reinterpret_cast<const uint16_t *>(wq)[o * cols + c]);
+  } else if constexpr (FMT == kINT8) {
+    return (float)(int8_t)wq[o * cols + c] * f16_to_f32(s[o * (cols / kGroup) + c / kGroup]);
+  } else {
+    const uint8_t b = wq[o * (cols / 2) + c / 2];
+    const int nib = (c % 2 == 0) ? (b >> 4) : (b & 0xf);
+    return ((float)nib - 8.0f) * f16_to_f32(s[o * (cols / kGroup) + c / kGroup]);
+  }
+}
+
+// out (rows, cols) f32.  With transposed, the matrix is stored as its (cols,
+// rows) transpose with groups of 32 along the stored columns' transpose: see
+// launch_relayout_transpose.
 template <int FMT>
 __global__ void __launch_bounds__(256) dequantize_kernel(const uint8_t *__restrict__ wq,
-                                                         const uint16_t *__restrict__ s, int rows,
-                                                         int cols, float *__restrict__ out) {
-#pragma clang fp contract(off)
+                                                         const uint16_t *__restrict__ s, int rows, int cols,
+                                                         bool transposed, float *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)rows * cols) return;
   const int64_t o = i / cols;
   const int c = (int)(i % cols);
+  if (!transposed) {
+    out[i] = stored_value<FMT>(wq, s, o, c, cols);
+    return;
+  }
+  // stored: element (o, c) of the logical matrix sits at (c, o) of a
+  // (cols, rows) matrix whose quantisation groups run down its columns
   float v;
   if constexpr (FMT == kF32) {
-    v = reinterpret_cast<const float *>(wq)[i];
+    v = reinterpret_cast<const float *>(wq)[(int64_t)c * rows + o];
   } else if constexpr (FMT == kBF16) {
-    v = bf16_to_f32(reinterpret_cast<const uint16_t *>(wq)[i]);
-  } else if constexpr (FMT == kINT8) {
-    v = (float)(int8_t)wq[i] * f16_to_f32(s[o * (cols / kGroup) + c / kGroup]);
+    v = bf16_to_f32(reinterpret_cast<const uint16_t *>(wq)[(int64_t)c * rows + o]);
   } else {
-    uint8_t b = wq[o * (cols / 2) + c / 2];
-    int nib = (c % 2 == 0) ? (b >> 4) : (b & 0xf);
-    v = ((float)nib - 8.0f) * f16_to_f32(s[o * (cols / kGroup) + c / kGroup]);
+    const float sc = f16_to_f32(s[(int64_t)(c / kGroup) * rows + o]);
+    if constexpr (FMT == kINT8) {
+      v = (float)(int8_t)wq[(int64_t)c * rows + o] * sc;
+    } else {
+      const uint8_t b = wq[(int64_t)c * (rows / 2) + o / 2];
+      const int nib = (o % 2 == 0) ? (b >> 4) : (b & 0xf);
+      v = ((float)nib - 8.0f) * sc;
+    }
   }
   out[i] = v;
 }
@@ -117,12 +147,77 @@ hipError_t launch_dequantize(const DevMat &m, int64_t index, float *out, hipStre
   dim3 grid((unsigned)((n + 255) / 256));
   const uint8_t *w = m.w + index * m.mat_bytes;
   const uint16_t *s = m.s ? m.s + index * m.mat_scales : nullptr;
+#define L(F) hipLaunchKernelGGL(dequantize_kernel<F>, grid, dim3(256), 0, st, w, s, m.rows, m.cols, m.transposed, out)
   switch (m.fmt) {
-  case kF32: hipLaunchKernelGGL(dequantize_kernel<kF32>, grid, dim3(256), 0, st, w, s, m.rows, m.cols, out); break;
-  case kBF16: hipLaunchKernelGGL(dequantize_kernel<kBF16>, grid, dim3(256), 0, st, w, s, m.rows, m.cols, out); break;
-  case kINT8: hipLaunchKernelGGL(dequantize_kernel<kINT8>, grid, dim3(256), 0, st, w, s, m.rows, m.cols, out); break;
-  default: hipLaunchKernelGGL(dequantize_kernel<kINT4>, grid, dim3(256), 0, st, w, s, m.rows, m.cols, out); break;
+  case kF32: L(kF32); break;
+  case kBF16: L(kBF16); break;
+  case kINT8: L(kINT8); break;
+  default: L(kINT4); break;
   }
+#undef L
+  return hipGetLastError();
+}
+
+// Re-layout of n_mat stored (rows, cols) matrices in the reference layout into
+// their (cols, rows) transposes, keeping every stored code and scale: the
+// element (o, c) moves to (c, o); INT4 nibbles pair up along the new rows
+// (even element in the high nibble); the group-32 scales (rows, cols / 32)
+// become (cols / 32, rows), one scale per (group, original row).  Values are
+// unchanged, so dequantisation stays bit-exact.
+template <int FMT>
+__global__ void __launch_bounds__(256) transpose_kernel(const uint8_t *__restrict__ src, const uint16_t *__restrict__ ss,
+                                                        int rows, int cols, uint8_t *__restrict__ dst,
+                                                        uint16_t *__restrict__ ds) {
+  const int64_t mat = blockIdx.y;
+  const int64_t mbytes = fmt_matrix_bytes(FMT, rows, cols);
+  const int64_t msc = fmt_quant(FMT) ? (int64_t)rows * (cols / kGroup) : 0;
+  src += mat * mbytes;
+  dst += mat * mbytes;
+  if constexpr (FMT == kINT4) {
+    // one thread per destination byte: (c, o pair)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)cols * (rows / 2)) return;
+    const int c = (int)(i / (rows / 2));
+    const int o = (int)(i % (rows / 2)) * 2;
+    auto nib = [&](int oo) {
+      const uint8_t b = src[(int64_t)oo * (cols / 2) + c / 2];
+      return (c % 2 == 0) ? (b >> 4) : (b & 0xf);
+    };
+    dst[i] = (uint8_t)((nib(o) << 4) | nib(o + 1));
+  } else {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // destination element (c, o)
+    if (i >= (int64_t)rows * cols) return;
+    const int c = (int)(i / rows);
+    const int o = (int)(i % rows);
+    if constexpr (FMT == kF32) {
+      reinterpret_cast<float *>(dst)[i] = reinterpret_cast<const float *>(src)[(int64_t)o * cols + c];
+    } else if constexpr (FMT == kBF16) {
+      reinterpret_cast<uint16_t *>(dst)[i] = reinterpret_cast<const uint16_t *>(src)[(int64_t)o * cols + c];
+    } else {
+      dst[i] = src[(int64_t)o * cols + c];
+    }
+  }
+  if constexpr (fmt_quant(FMT)) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // destination scale (g, o)
+    if (i < msc) {
+      const int g = (int)(i / rows), o = (int)(i % rows);
+      ds[mat * msc + i] = ss[mat * msc + (int64_t)o * (cols / kGroup) + g];
+    }
+  }
+}
+
+hipError_t launch_relayout_transpose(int fmt, const uint8_t *src, const uint16_t *ss, int64_t n_mat, int rows,
+                                     int cols, uint8_t *dst, uint16_t *ds, hipStream_t st) {
+  const int64_t n = (int64_t)rows * cols;
+  dim3 grid((unsigned)((n + 255) / 256), (unsigned)n_mat);
+#define L(F) hipLaunchKernelGGL(transpose_kernel<F>, grid, dim3(256), 0, st, src, ss, rows, cols, dst, ds)
+  switch (fmt) {
+  case kF32: L(kF32); break;
+  case kBF16: L(kBF16); break;
+  case kINT8: L(kINT8); break;
+  default: L(kINT4); break;
+  }
+#undef L
   return hipGetLastError();
 }
 

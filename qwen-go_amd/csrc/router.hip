@@ -331,7 +331,7 @@ __global__ void __launch_bounds__(256) select_cert_kernel(const float *__restric
   if (ok) return;
   for (int i = threadIdx.x; i < H; i += 256) xs[i] = x[(size_t)t * H + i];
   __syncthreads();
-  exact_logits_block(xs, H, router.w, router.s, router.fmt, E, lt);
+  exact_logits_block(xs, H, router.w, router.s, router.fmt, E, lt, 256);
   __syncthreads();
   if (threadIdx.x < 64)
     select_exact_nj<NJ>(lt, E, k, scope, ids + (size_t)t * k, weights + (size_t)t * k, nullptr, nullptr);

@@ -215,10 +215,13 @@ __device__ __forceinline__ double wave_max_f64(double v) { return dkey_inv(wave_
 // size of |L - max| plus 2^-20, with |L - max| < 80 so that no probability is
 // subnormal.  An order that the f32 keys got wrong, or any near or exact tie,
 // fails certification; the function then returns false and writes nothing.
-// Weights come from the f64 softmax of S.
+// Weights come from the f64 softmax of S.  When spec_slot is given, the
+// tentative expert of rank spec_rank is published there (as id + 1) as soon
+// as its round ends, before certification.
 template <int NJ>
 __device__ __forceinline__ bool certified_select_nj(const double *__restrict__ sb, int E, int k, int scope,
-                                                    int32_t *g_ids, float *g_w, int *s_ids, float *s_w) {
+                                                    int32_t *g_ids, float *g_w, int *s_ids, float *s_w,
+                                                    int spec_rank = -1, volatile int *spec_slot = nullptr) {
   const int lane = threadIdx.x & 63;
   double S[NJ], B[NJ];
   float key[NJ];
@@ -238,7 +241,8 @@ __device__ __forceinline__ bool certified_select_nj(const double *__restrict__ s
     key[j] = e < scope ? (float)S[j] : -INFINITY;
   }
   // upper bound of the reference's max logit (f32 rounding covered by 2^-20)
-  const double mx_hi = (double)wave_max_f32(mh) * (1.0 + 0x1p-20) + 0x1p-60;
+  const double mh_all = (double)wave_max_f32(mh);
+  const double mx_hi = mh_all + fabs(mh_all) * 0x1p-20 + 0x1p-60;
   int lj = -1;
   float lbest = -INFINITY;
 #pragma unroll
@@ -272,6 +276,7 @@ __device__ __forceinline__ bool certified_select_nj(const double *__restrict__ s
       myS = sc;
       myB = bc;
     }
+    if (r == spec_rank && lane == 0) *spec_slot = c + 1;  // tentative expert of that rank
     if (lane == wl) {  // the winner's lane drops it and refreshes its best
 #pragma unroll
       for (int j = 0; j < NJ; j++)
@@ -346,13 +351,14 @@ __device__ __forceinline__ bool certified_select_nj(const double *__restrict__ s
 
 // Exact sequential logits (model/tensors.go:77-89, model/model.go:167-176,
 // model/moe.go:159-162) of one token for every expert, computed by the whole
-// block into lt, with a run-time format switch (slow path only).
+// first nthreads threads of the block into lt, with a run-time format switch
+// (slow path only).
 __device__ __forceinline__ void exact_logits_block(const float *__restrict__ xs, int H, const uint8_t *__restrict__ w,
                                                    const uint16_t *__restrict__ sc, int fmt, int E,
-                                                   float *__restrict__ lt) {
+                                                   float *__restrict__ lt, int nthreads) {
 #pragma clang fp contract(off)
   const int64_t row_bytes = fmt_matrix_bytes(fmt, 1, H);
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+  for (int e = threadIdx.x; e < E; e += nthreads) {
     const uint8_t *row = w + (size_t)e * row_bytes;
     const uint16_t *srow = fmt_quant(fmt) ? sc + (size_t)e * (H / kGroup) : nullptr;
     float acc = 0.0f;
