@@ -40,7 +40,8 @@ hipError_t launch_softmax_select(const float *logits, int T, int E, int k, int s
                                  int32_t *ids, float *weights, hipStream_t st);
 
 // ---- expert products (fused.hip) ----
-// One kernel per (token, rank, 32 intermediate rows): the block's expert (from
+// One kernel per forward; each block takes an equal share of a token's
+// flattened intermediate rows (k*I routed + Is shared): its experts (from
 // the router partials sb with certification, or from precomputed ids/weights
 // when sb is null), gate_up + SwiGLU, and the matching rows of the transposed
 // down matrix, accumulated into out with f32 atomics.  out must be zero on
@@ -64,7 +65,8 @@ struct FusedArgs {
   unsigned int *fallbacks;
   float *out;                         // (T, H), accumulated
   int k_routed, with_shared;          // ranks of this launch
-  int nchunks, ranks;                 // filled by the launcher
+  int n_cu;                           // compute units of the device
+  int nb, rb;                         // filled by the launcher: blocks per token, rows per block
 };
 hipError_t launch_expert_fused(const FusedArgs &a, hipStream_t st);
 bool fused_supported(int fmt, int H, int E);  // the LDS plan fits

@@ -40,6 +40,7 @@ struct DevBuf {
 struct qmoe_layer {
   qmoe_desc d{};
   int scope = 0;
+  int n_cu = 256;  // compute units of the device
   std::mutex mu;
   std::string err = "no error";
   bool destroyed = false;
@@ -321,6 +322,7 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   f.out = d_out;
   f.k_routed = k;
   f.with_shared = Is > 0 && d.shared_fmt == d.expert_fmt;
+  f.n_cu = l->n_cu;
   STAGE(l, QMOE_STAGE_FUSED, st, launch_expert_fused(f, st), "fused expert launch");
   if (Is > 0 && d.shared_fmt != d.expert_fmt) {
     // shared expert in its own format: a second launch of the same kernel
@@ -382,6 +384,11 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
 
   qmoe_layer *l = new qmoe_layer();
   l->d = d;
+  {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, d.device) == hipSuccess && prop.multiProcessorCount > 0)
+      l->n_cu = prop.multiProcessorCount;
+  }
   l->scope = d.select_scope == 0 ? d.top_k : d.select_scope;
   e = hipStreamCreate(&l->stream);
   if (e != hipSuccess) {

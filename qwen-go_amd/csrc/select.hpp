@@ -221,7 +221,8 @@ __device__ __forceinline__ double wave_max_f64(double v) { return dkey_inv(wave_
 template <int NJ>
 __device__ __forceinline__ bool certified_select_nj(const double *__restrict__ sb, int E, int k, int scope,
                                                     int32_t *g_ids, float *g_w, int *s_ids, float *s_w,
-                                                    int spec_rank = -1, volatile int *spec_slot = nullptr) {
+                                                    int spec_rank = -1, int *spec_slot = nullptr) {
+  // spec_rank == -2: publish every rank's tentative expert to spec_slot[rank]
   const int lane = threadIdx.x & 63;
   double S[NJ], B[NJ];
   float key[NJ];
@@ -276,7 +277,12 @@ __device__ __forceinline__ bool certified_select_nj(const double *__restrict__ s
       myS = sc;
       myB = bc;
     }
-    if (r == spec_rank && lane == 0) *spec_slot = c + 1;  // tentative expert of that rank
+    if (lane == 0) {  // tentative expert of that rank (spec_slot is in LDS)
+      if (spec_rank == -2)
+        __hip_atomic_store(spec_slot + r, c + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      else if (r == spec_rank)
+        __hip_atomic_store(spec_slot, c + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     if (lane == wl) {  // the winner's lane drops it and refreshes its best
 #pragma unroll
       for (int j = 0; j < NJ; j++)
