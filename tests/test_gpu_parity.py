@@ -215,6 +215,32 @@ def test_router_exact_ties(T):
         assert fb >= T  # every token hit a tie
 
 
+@pytest.mark.parametrize("scope_tag", ["E", "k"])
+def test_golden_tiny_layer(scope_tag):
+    """The committed float64 evaluation (tests/golden/tiny_layer.npz, f32
+    weights, shared expert): ids exact, output within 1e-3 normwise."""
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_layer.npz")
+    with np.load(path) as z:
+        t = {k: z[k] for k in z.files}
+    E, H = t["router"].shape
+    I, Is, k = t["gate_up"].shape[1] // 2, t["sh_gate"].shape[0], t["ids_E"].shape[1]
+    scope = E if scope_tag == "E" else k
+    announce(f"golden tiny layer scope={scope_tag}")
+    cfg = qmoe.LayerConfig(H, E, k, I, Is, scope, qmoe.F32, qmoe.F32, qmoe.F32, "golden")
+    hw = qmoe.HostWeights(cfg, t["router"], None, t["gate_up"], None, t["down"], None, t["sh_gate"], None,
+                          t["sh_up"], None, t["sh_down"], None, t["shared_gate"])
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(t["x"])
+    finally:
+        layer.close()
+    assert np.array_equal(ids, t[f"ids_{scope_tag}"])
+    np.testing.assert_allclose(w, t[f"w_{scope_tag}"], rtol=1e-5)
+    assert rel_err(out, t[f"out_{scope_tag}"]) <= TOL_F32
+
+
 # ----------------------------------------------------------- contract
 
 def test_contract_errors():
