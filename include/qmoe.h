@@ -134,12 +134,26 @@ qmoe_status qmoe_dequant_debug(qmoe_layer *layer, int32_t which, int32_t expert,
 enum {
     QMOE_STAGE_ROUTER = 0,         /* router logits */
     QMOE_STAGE_SELECT = 1,         /* softmax + selection + renormalisation */
-    QMOE_STAGE_GATE_UP = 2,        /* routed experts gate_up + SwiGLU */
-    QMOE_STAGE_SHARED_GATE_UP = 3, /* shared expert gate_up + SwiGLU + gate */
-    QMOE_STAGE_DOWN = 4,           /* down + weighted combine + shared */
+    QMOE_STAGE_GATE_UP = 2,        /* batched: routed experts gate_up + SwiGLU (MFMA) */
+    QMOE_STAGE_SHARED_GATE_UP = 3, /* batched: shared expert gate_up + SwiGLU (MFMA) */
+    QMOE_STAGE_DOWN = 4,           /* batched: down of routed and shared experts (MFMA) */
     QMOE_STAGE_FUSED = 5,          /* decode: routing + gate_up + down in one kernel */
+    QMOE_STAGE_DISPATCH = 6,       /* batched: x to bf16, shared gate, per-expert token lists */
+    QMOE_STAGE_COMBINE = 7,        /* batched: rank-order sum of the expert outputs + shared */
     QMOE_STAGE_COUNT = 8
 };
+
+/* Which kernels a forward of T tokens runs, with no reference counterpart
+ * (the reference has one CPU path):
+ *   QMOE_PATH_GEMV  decode kernels, f32 activations and accumulation (parity
+ *                   bar 1e-3 normwise against model/moe.go);
+ *   QMOE_PATH_MFMA  dispatch + grouped GEMMs on bf16 MFMA with f32
+ *                   accumulation, x and the SwiGLU output rounded to bf16
+ *                   (parity bar 2e-2 normwise).
+ * The router and the selection are exact on both paths, so expert ids always
+ * match the reference bit for bit.  Returns -1 for a null handle. */
+enum { QMOE_PATH_GEMV = 0, QMOE_PATH_MFMA = 1 };
+int32_t qmoe_forward_path(const qmoe_layer *layer, int32_t T);
 
 /* Instrumentation with no reference counterpart (the reference has no
  * timers): when bit s of stage_mask is set, every later forward records a HIP

@@ -72,6 +72,37 @@ hipError_t launch_expert_fused(const FusedArgs &a, hipStream_t st);
 bool fused_supported(int fmt, int H, int E);  // the LDS plan fits
 hipError_t launch_zero(float *p, int64_t n, hipStream_t st);
 
+// ---- prefill: dispatch, grouped MFMA GEMMs, combine (prefill.hip) ----
+// Slots: the T*k (token, rank) pairs grouped by expert, then the shared
+// expert's T slots (group E) in token order.
+struct PrefillPlan {
+  int32_t *tok;                 // (slots) token of each slot
+  float *wslot;                 // (slots) routing weight, or the shared gate
+  int32_t *slot_of;             // (T, k) slot of each (token, rank)
+  int32_t *grp_off, *grp_cnt;   // (E + 1) first slot and slot count per group
+  int32_t *tile_grp, *tile_m0;  // tile table: group and first row of each 128-slot tile
+  int32_t *n_tiles;             // [0] routed tiles, [1] shared tiles (after the routed ones)
+};
+struct PrefillArgs {
+  int T, H, E, k, I, Is, Imax;  // Imax = max(I, Is), the row pitch of act
+  uint16_t *xb;                 // (T, H) x in bf16
+  PrefillPlan p;
+  const uint8_t *gu, *dn;       // gate_up (E, 2I, H); down transposed (E, I, H)
+  const uint16_t *gu_s, *dn_s;
+  int64_t gu_bytes, gu_scales, dn_bytes, dn_scales;
+  const uint8_t *sgate, *sup, *sdown;
+  const uint16_t *sgate_s, *sup_s, *sdown_s;
+  uint16_t *act;                // (slots, Imax) SwiGLU output, bf16
+  float *y;                     // (slots, H) weighted expert outputs
+};
+bool prefill_supported(int expert_fmt, int shared_fmt, int H, int I, int Is);
+int prefill_max_tiles(int T, int k, int E);  // routed tiles, upper bound
+hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, const float *wts, const float *x,
+                                   const float *shared_gate, float *sg, hipStream_t st);
+hipError_t launch_prefill_gate_up(const PrefillArgs &a, bool shared, hipStream_t st);
+hipError_t launch_prefill_down(const PrefillArgs &a, bool shared, hipStream_t st);
+hipError_t launch_prefill_combine(const PrefillArgs &a, float *out, hipStream_t st);
+
 // ---- quantiser / dequantiser (quant.hip) ----
 hipError_t launch_quantize(int bits, const float *w, int64_t n_rows, int cols, uint8_t *codes,
                            uint16_t *scales, hipStream_t st);

@@ -59,6 +59,11 @@ struct qmoe_layer {
   float *xbuf = nullptr, *obuf = nullptr;
   double *sb = nullptr;
   int32_t *ids = nullptr;
+  // batched (MFMA) path buffers, present when ws_mfma
+  bool ws_mfma = false;
+  uint16_t *xb = nullptr, *act = nullptr;
+  float *sg = nullptr, *y = nullptr;
+  PrefillPlan plan{};
   unsigned int *fallbacks = nullptr;  // tokens routed by the exact fallback
 
   // optional per-stage event timing (qmoe_profile_*)
@@ -232,10 +237,20 @@ hipError_t next_event(qmoe_layer *l, hipEvent_t *ev) {
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
-qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
-  if (T <= l->ws_T) return QMOE_OK;
+// Token counts above this run the batched MFMA path when its formats allow.
+constexpr int kMaxGemvTokens = 32;
+
+bool use_mfma(const qmoe_layer *l, int T) {
   const qmoe_desc &d = l->d;
-  int nT = std::max(T, 64);
+  return T > kMaxGemvTokens &&
+         prefill_supported(d.expert_fmt, d.shared_fmt, d.hidden, d.moe_inter, d.shared_inter);
+}
+
+qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
+  const bool mfma = use_mfma(l, T);
+  if (T <= l->ws_T && (!mfma || l->ws_mfma)) return QMOE_OK;
+  const qmoe_desc &d = l->d;
+  int nT = std::max(std::max(T, l->ws_T), 64);
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes); return o; };
   size_t o_logits = take((size_t)nT * d.n_experts * 4);
@@ -244,6 +259,26 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_x = take((size_t)nT * d.hidden * 4);
   size_t o_o = take((size_t)nT * d.hidden * 4);
   size_t o_sb = take((size_t)nT * d.n_experts * 16);
+  const bool want_mfma = mfma || l->ws_mfma;
+  const size_t pairs = (size_t)nT * d.top_k, slots = pairs + (size_t)nT;
+  const size_t tiles = (size_t)prefill_max_tiles(nT, d.top_k, d.n_experts) + (nT + 127) / 128;
+  const int imax = std::max(d.moe_inter, d.shared_inter);
+  size_t o_xb = 0, o_sg = 0, o_tok = 0, o_wsl = 0, o_slot = 0, o_goff = 0, o_gcnt = 0, o_tg = 0, o_tm = 0,
+         o_nt = 0, o_act = 0, o_y = 0;
+  if (want_mfma) {
+    o_xb = take((size_t)nT * d.hidden * 2);
+    o_sg = take((size_t)nT * 4);
+    o_tok = take(slots * 4);
+    o_wsl = take(slots * 4);
+    o_slot = take(pairs * 4);
+    o_goff = take((size_t)(d.n_experts + 1) * 4);
+    o_gcnt = take((size_t)(d.n_experts + 1) * 4);
+    o_tg = take(tiles * 4);
+    o_tm = take(tiles * 4);
+    o_nt = take(2 * 4);
+    o_act = take(slots * imax * 2);
+    o_y = take(slots * d.hidden * 4);
+  }
   // Pending work of earlier calls may still read the old workspace.
   if (user_stream) HIP_TRY(l, hipStreamSynchronize(user_stream), "hipStreamSynchronize");
   HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
@@ -263,6 +298,21 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   l->xbuf = (float *)(b + o_x);
   l->obuf = (float *)(b + o_o);
   l->sb = (double *)(b + o_sb);
+  l->ws_mfma = want_mfma;
+  if (want_mfma) {
+    l->xb = (uint16_t *)(b + o_xb);
+    l->sg = (float *)(b + o_sg);
+    l->plan.tok = (int32_t *)(b + o_tok);
+    l->plan.wslot = (float *)(b + o_wsl);
+    l->plan.slot_of = (int32_t *)(b + o_slot);
+    l->plan.grp_off = (int32_t *)(b + o_goff);
+    l->plan.grp_cnt = (int32_t *)(b + o_gcnt);
+    l->plan.tile_grp = (int32_t *)(b + o_tg);
+    l->plan.tile_m0 = (int32_t *)(b + o_tm);
+    l->plan.n_tiles = (int32_t *)(b + o_nt);
+    l->act = (uint16_t *)(b + o_act);
+    l->y = (float *)(b + o_y);
+  }
   l->ws_T = nT;
   return QMOE_OK;
 }
@@ -276,7 +326,51 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   float *wts = d_w ? d_w : l->wts;
   const int H = d.hidden, E = d.n_experts, k = d.top_k, I = d.moe_inter, Is = d.shared_inter;
 
-  const bool cert = T <= 32 && router_certified_supported(l->router);
+  if (use_mfma(l, T)) {
+    // batched path: exact router and selection, then dispatch, grouped GEMMs, combine
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
+    STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st),
+          "softmax/select launch");
+    PrefillArgs pa{};
+    pa.T = T;
+    pa.H = H;
+    pa.E = E;
+    pa.k = k;
+    pa.I = I;
+    pa.Is = Is;
+    pa.Imax = std::max(I, Is);
+    pa.xb = l->xb;
+    pa.p = l->plan;
+    pa.gu = l->gu.w;
+    pa.dn = l->dn.w;
+    pa.gu_s = l->gu.s;
+    pa.dn_s = l->dn.s;
+    pa.gu_bytes = l->gu.mat_bytes;
+    pa.gu_scales = l->gu.mat_scales;
+    pa.dn_bytes = l->dn.mat_bytes;
+    pa.dn_scales = l->dn.mat_scales;
+    if (Is > 0) {
+      pa.sgate = l->sgate.w;
+      pa.sup = l->sup.w;
+      pa.sdown = l->sdown.w;
+      pa.sgate_s = l->sgate.s;
+      pa.sup_s = l->sup.s;
+      pa.sdown_s = l->sdown.s;
+    }
+    pa.act = l->act;
+    pa.y = l->y;
+    STAGE(l, QMOE_STAGE_DISPATCH, st, launch_prefill_dispatch(pa, ids, wts, d_x, l->shared_gate, l->sg, st),
+          "dispatch launch");
+    STAGE(l, QMOE_STAGE_GATE_UP, st, launch_prefill_gate_up(pa, false, st), "gate_up launch");
+    if (Is > 0)
+      STAGE(l, QMOE_STAGE_SHARED_GATE_UP, st, launch_prefill_gate_up(pa, true, st), "shared gate_up launch");
+    STAGE(l, QMOE_STAGE_DOWN, st, launch_prefill_down(pa, false, st), "down launch");
+    if (Is > 0) STAGE(l, QMOE_STAGE_DOWN, st, launch_prefill_down(pa, true, st), "shared down launch");
+    STAGE(l, QMOE_STAGE_COMBINE, st, launch_prefill_combine(pa, d_out, st), "combine launch");
+    return QMOE_OK;
+  }
+
+  const bool cert = T <= kMaxGemvTokens && router_certified_supported(l->router);
   if (cert) {
     STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, d_out, st), "router launch");
   } else {
@@ -654,6 +748,11 @@ qmoe_status qmoe_router_fallbacks(qmoe_layer *l, int64_t *count) {
   HIP_TRY(l, hipMemcpy(&v, l->fallbacks, sizeof(v), hipMemcpyDeviceToHost), "fallback counter read");
   *count = v;
   return QMOE_OK;
+}
+
+int32_t qmoe_forward_path(const qmoe_layer *l, int32_t T) {
+  if (!l) return -1;
+  return use_mfma(l, T) ? QMOE_PATH_MFMA : QMOE_PATH_GEMV;
 }
 
 int64_t qmoe_device_bytes(const qmoe_layer *l) {

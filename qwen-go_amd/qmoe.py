@@ -66,6 +66,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_forward_device": ([vp, vp, i32, vp, vp, vp, vp], i32),
         "qmoe_dequant_debug": ([vp, i32, i32, vp], i32),
         "qmoe_device_bytes": ([vp], i64),
+        "qmoe_forward_path": ([vp, i32], i32),
         "qmoe_profile_enable": ([vp, ctypes.c_uint32], i32),
         "qmoe_profile_read": ([vp, vp, vp, i32], i32),
         "qmoe_router_fallbacks": ([vp, vp], i32),
@@ -85,11 +86,13 @@ def exported_symbols() -> list[str]:
             "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks"]
 
 
-STAGE_ROUTER, STAGE_SELECT, STAGE_GATE_UP, STAGE_SHARED_GATE_UP, STAGE_DOWN, STAGE_FUSED = range(6)
+(STAGE_ROUTER, STAGE_SELECT, STAGE_GATE_UP, STAGE_SHARED_GATE_UP, STAGE_DOWN, STAGE_FUSED, STAGE_DISPATCH,
+ STAGE_COMBINE) = range(8)
 STAGE_COUNT = 8
 STAGE_NAMES = {STAGE_ROUTER: "router_logits", STAGE_SELECT: "softmax_select",
                STAGE_GATE_UP: "gate_up", STAGE_SHARED_GATE_UP: "shared_gate_up", STAGE_DOWN: "down",
-               STAGE_FUSED: "fused_experts"}
+               STAGE_FUSED: "fused_experts", STAGE_DISPATCH: "dispatch", STAGE_COMBINE: "combine"}
+PATH_GEMV, PATH_MFMA = 0, 1
 
 
 def _ptr(a):
@@ -229,6 +232,10 @@ class MoeLayer:
 
     def device_bytes(self) -> int:
         return int(self.lib.qmoe_device_bytes(self.h))
+
+    def forward_path(self, T: int) -> int:
+        """PATH_GEMV (f32 activations) or PATH_MFMA (bf16 MFMA) for T tokens."""
+        return int(self.lib.qmoe_forward_path(self.h, T))
 
     def close(self):
         if getattr(self, "h", None) is not None and self.h.value:

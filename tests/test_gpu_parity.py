@@ -241,6 +241,83 @@ def test_golden_tiny_layer(scope_tag):
     assert rel_err(out, t[f"out_{scope_tag}"]) <= TOL_F32
 
 
+# ------------------------------------------------- batched (MFMA) path
+
+TOL_MFMA = 2e-2  # x and the SwiGLU output rounded to bf16, f32 accumulation
+
+
+def check_mfma_layer(cfg, hw, x, scope=None):
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        assert layer.forward_path(x.shape[0]) == qmoe.PATH_MFMA
+        out, ids, w = layer.forward(x)
+    finally:
+        layer.close()
+    ref, rids, rw = oracle.OracleLayer(hw, scope=scope, threads=8).forward(x)
+    assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
+    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
+    err = rel_err(out, ref)
+    assert err <= TOL_MFMA, f"normwise relative error {err:.3e} > {TOL_MFMA}"
+    return out, ids, err
+
+
+PREFILL = [
+    # (router fmt, shared_inter, scope)
+    (qmoe.BF16, 0, 0),
+    (qmoe.BF16, 64, 16),
+    (qmoe.F32, 128, 0),
+]
+
+
+@pytest.mark.parametrize("fmts", PREFILL, ids=lambda f: "-".join(map(str, f)))
+@pytest.mark.parametrize("T", [33, 100, 300])
+def test_prefill_layers(fmts, T):
+    rf, Is, scope = fmts
+    cfg = qmoe.LayerConfig(256, 16, 4, 128, Is, scope, rf, qmoe.BF16, qmoe.BF16, "prefill")
+    announce(f"prefill layer fmts={fmts} T={T}")
+    hw = qmoe.synthetic_weights(cfg, 300 + T, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, T, 300 + T)
+    check_mfma_layer(cfg, hw, x)
+
+
+def test_prefill_skewed_routing():
+    """One expert takes most tokens (several 128-slot tiles), most take none."""
+    cfg = qmoe.LayerConfig(256, 16, 2, 128, 64, 16, qmoe.BF16, qmoe.BF16, qmoe.BF16, "skew")
+    announce("prefill skewed routing T=400")
+    hw = qmoe.synthetic_weights(cfg, 41, quantizer=oracle.host_quantizer, router_scale=4.0)
+    x = qmoe.synthetic_tokens(cfg, 400, 41)
+    r = qmoe.bf16_bits_to_f32(hw.router).reshape(16, 256).astype(np.float32)
+    x = (x + 3.0 * r[5] / np.linalg.norm(r[5]) * np.sqrt(256)).astype(np.float32)
+    out, ids, _ = check_mfma_layer(cfg, hw, x)
+    counts = np.bincount(ids.reshape(-1), minlength=16)
+    assert counts.max() > 256, counts  # the hot expert spans three tiles
+
+
+def test_prefill_qwen3_shape_rows_are_independent():
+    """Qwen3-30B-A3B shape: T=64 against the oracle, then T=2048 (sharpened
+    router) whose first 64 rows must equal the T=64 result bit for bit -- each
+    token's output depends on its own row only, whatever the dispatch order."""
+    cfg = qmoe.CONFIGS["qwen3_30b_a3b"].with_(select_scope=128)
+    announce("prefill qwen3-30b-a3b bf16 T=64 vs oracle, T=2048 row independence")
+    hw = qmoe.synthetic_weights(cfg, 2048, quantizer=oracle.host_quantizer, router_scale=4.0)
+    x = qmoe.synthetic_tokens(cfg, 2048, 2048)
+    out64, ids64, _ = check_mfma_layer(cfg, hw, x[:64])
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(x)
+        perm = np.random.default_rng(1).permutation(2048)
+        outp, idsp, _ = layer.forward(np.ascontiguousarray(x[perm]))
+    finally:
+        layer.close()
+    assert np.array_equal(ids[:64], ids64)
+    assert np.array_equal(out[:64].view(np.uint32), out64.view(np.uint32))
+    assert np.array_equal(idsp, ids[perm])
+    assert np.array_equal(outp.view(np.uint32), out[perm].view(np.uint32))
+    assert np.all(np.isfinite(out))
+
+
 # ----------------------------------------------------------- contract
 
 def test_contract_errors():
