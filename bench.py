@@ -39,6 +39,8 @@ WORKLOADS = {
     # name: (config key, T, scope, description)
     "decode": ("qwen3_30b_a3b", 1, "E", "qwen3-30b-a3b moe layer decode T=1, bf16 weights, top-8 of 128"),
     "decode8": ("qwen3_30b_a3b", 8, "E", "qwen3-30b-a3b moe layer decode T=8, bf16 weights, top-8 of 128"),
+    "prefill": ("qwen3_30b_a3b", 2048, "E",
+                "qwen3-30b-a3b moe layer prefill T=2048, bf16 weights, router x4, skewed tokens, top-8 of 128"),
     "int8_decode": ("qwen3_30b_a3b_int8", 1, "E",
                     "qwen3-30b-a3b moe layer decode T=1, int8 group-32 experts, top-8 of 128"),
     "next_decode": ("qwen3_next", 1, "E",
@@ -57,7 +59,50 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--skew", type=float, default=10.0,
+                    help="prefill: target ratio of the busiest expert's load to the median load")
     return ap.parse_args()
+
+
+# prefill workloads: router weights x4 and tokens pulled along one direction
+ROUTER_SCALE = {"prefill": 4.0}
+
+
+def skewed_tokens(cfg, hw, T, seed, target):
+    """x_t = z_t + c u with a fixed random unit direction u; c is chosen on the
+    host (router logits in float64) so that the busiest expert receives about
+    `target` times the median expert's load.  Returns (x, c, load stats)."""
+    rng = np.random.default_rng(seed)
+    u = rng.standard_normal(cfg.hidden)
+    u /= np.linalg.norm(u)
+    z = qmoe.synthetic_tokens(cfg, T, seed)
+    if cfg.router_fmt == qmoe.BF16:
+        r = qmoe.bf16_bits_to_f32(hw.router).astype(np.float64)
+    else:
+        r = np.asarray(hw.router, np.float64)
+    r = r.reshape(cfg.n_experts, cfg.hidden)
+    zl, ul = z.astype(np.float64) @ r.T, r @ u
+
+    def load(c):
+        lg = zl + c * ul
+        top = np.argsort(-lg, axis=1, kind="stable")[:, :cfg.top_k]
+        return np.bincount(top.reshape(-1), minlength=cfg.n_experts)
+
+    def ratio(c):
+        n = load(c)
+        return n.max() / max(np.median(n), 1.0)
+
+    lo, hi = 0.0, 64.0
+    if ratio(lo) < target:
+        for _ in range(30):
+            mid = 0.5 * (lo + hi)
+            lo, hi = (mid, hi) if ratio(mid) < target else (lo, mid)
+    c = hi if ratio(lo) < target else lo
+    n = load(c)
+    x = (z + c * u[None, :]).astype(np.float32)
+    stats = {"c": round(float(c), 3), "max_load": int(n.max()), "median_load": float(np.median(n)),
+             "min_load": int(n.min()), "experts_used": int((n > 0).sum())}
+    return x, stats
 
 
 def stage_bytes(cfg, T, ids):
@@ -68,12 +113,20 @@ def stage_bytes(cfg, T, ids):
     b = {
         qmoe.STAGE_ROUTER: wb(cfg.router_fmt, E, H) + T * H * 4 + T * E * 4,
         qmoe.STAGE_SELECT: T * E * 4 + T * k * 8,
-        qmoe.STAGE_GATE_UP: touched * wb(cfg.expert_fmt, 2 * I, H) + T * H * 4 + T * k * I * 4,
-        qmoe.STAGE_DOWN: touched * wb(cfg.expert_fmt, H, I) + T * k * I * 4 + T * k * 8 + T * H * 4,
+        # batched path: weights + bf16 x rows in + bf16 SwiGLU rows out
+        qmoe.STAGE_GATE_UP: touched * wb(cfg.expert_fmt, 2 * I, H) + T * H * 2 + T * k * I * 2,
+        # weights + bf16 SwiGLU rows in + f32 weighted rows out
+        qmoe.STAGE_DOWN: touched * wb(cfg.expert_fmt, H, I) + T * k * I * 2 + T * k * H * 4,
+        # x in, bf16 x out, ids/weights in, slot tables out
+        qmoe.STAGE_DISPATCH: T * H * 4 + T * H * 2 + T * k * 8 + T * k * 12,
+        # f32 weighted rows in, out
+        qmoe.STAGE_COMBINE: T * k * H * 4 + T * H * 4,
     }
     if Is:
-        b[qmoe.STAGE_SHARED_GATE_UP] = 2 * wb(cfg.shared_fmt, Is, H) + H * 4 + T * H * 4 + T * Is * 4 + T * 4
-        b[qmoe.STAGE_DOWN] += wb(cfg.shared_fmt, H, Is) + T * Is * 4 + T * 4
+        b[qmoe.STAGE_SHARED_GATE_UP] = 2 * wb(cfg.shared_fmt, Is, H) + T * H * 2 + T * Is * 2
+        b[qmoe.STAGE_DOWN] += wb(cfg.shared_fmt, H, Is) + T * Is * 2 + T * H * 4
+        b[qmoe.STAGE_DISPATCH] += H * 4
+        b[qmoe.STAGE_COMBINE] += T * H * 4
     # decode: one kernel reads the routed (and shared) gate_up and down weights,
     # x and the router partials, and accumulates out
     b[qmoe.STAGE_FUSED] = (touched * (wb(cfg.expert_fmt, 2 * I, H) + wb(cfg.expert_fmt, H, I)) + T * H * 4
@@ -83,23 +136,36 @@ def stage_bytes(cfg, T, ids):
     return b
 
 
+def stage_flops(cfg, T):
+    """MFMA flops of the batched GEMMs for one forward of T tokens."""
+    H, k, I, Is = cfg.hidden, cfg.top_k, cfg.moe_inter, cfg.shared_inter
+    f = {qmoe.STAGE_GATE_UP: 2 * T * k * 2 * I * H, qmoe.STAGE_DOWN: 2 * T * k * H * I}
+    if Is:
+        f[qmoe.STAGE_SHARED_GATE_UP] = 2 * T * 2 * Is * H
+        f[qmoe.STAGE_DOWN] += 2 * T * H * Is
+    return f
+
+
 def cpu_baseline(hw, cfg, T, scope, xs, budget_s):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     threads = min(os.cpu_count() or 1, 8)
     ol = oracle.OracleLayer(hw, scope=scope, threads=threads)
-    x = xs[0][:T]
+    # per-token cost is independent of T (one forward per token, model.go:508-514):
+    # a bounded slice of at most 32 tokens per call
+    Tc = min(T, 32)
+    x = xs[0][:Tc]
     t0 = time.perf_counter()
     ol.forward(x)
     one = time.perf_counter() - t0
     reps = max(2, min(400, int(budget_s / max(one, 1e-6))))
     t0 = time.perf_counter()
     for i in range(reps):
-        ol.forward(xs[i % len(xs)][:T])
+        ol.forward(xs[i % len(xs)][:Tc])
     dt = time.perf_counter() - t0
     return {
-        "value": round(reps * T / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-        "sample": (f"{reps} forwards of T={T} ({reps * T} tokens) of the same layer and routing, "
+        "value": round(reps * Tc / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": (f"{reps} forwards of T={Tc} ({reps * Tc} tokens) of the same layer and routing, "
                    f"C restatement of model/moe.go (gcc -O2 -ffp-contract=off), one call per token as "
                    f"decodeLayers does; router/shared bf16 GEMVs on {threads} threads "
                    f"(GOMAXPROCS-equivalent min(nproc,8)), expert GEMVs single-threaded; Go is not "
@@ -125,7 +191,7 @@ def main():
     sptr = stream.cuda_stream
 
     t_gen = time.perf_counter()
-    hw = qmoe.synthetic_weights(cfg, args.seed)
+    hw = qmoe.synthetic_weights(cfg, args.seed, router_scale=ROUTER_SCALE.get(args.workload, 1.0))
     lb = qmoe.layer_bytes(cfg)
     layer_total = lb["router"] + cfg.n_experts * lb["per_expert"] + lb["shared"]
     step_bytes_est = lb["router"] + min(cfg.n_experts, T * cfg.top_k) * lb["per_expert"] + lb["shared"]
@@ -137,8 +203,17 @@ def main():
         layers.append(L)
     gen_s = time.perf_counter() - t_gen
 
-    n_x = 64
-    xs_host = [qmoe.synthetic_tokens(cfg, T, args.seed + 1000 + i) for i in range(n_x)]
+    n_x = max(2, min(64, (1 << 24) // (T * cfg.hidden)))
+    skew = None
+    if args.workload in ROUTER_SCALE:
+        xs_host, stats = [], []
+        for i in range(n_x):
+            x, st = skewed_tokens(cfg, hw, T, args.seed + 1000 + i, args.skew)
+            xs_host.append(x)
+            stats.append(st)
+        skew = {"target_max_over_median": args.skew, "per_x": stats}
+    else:
+        xs_host = [qmoe.synthetic_tokens(cfg, T, args.seed + 1000 + i) for i in range(n_x)]
     d_x = torch.from_numpy(np.stack(xs_host)).to(dev).contiguous()   # (n_x, T, H)
     d_out = torch.empty((T, cfg.hidden), dtype=torch.float32, device=dev)
     d_ids = torch.empty((n_x, T, cfg.top_k), dtype=torch.int32, device=dev)
@@ -160,7 +235,7 @@ def main():
     per_x_bytes = [stage_bytes(cfg, T, ids_all[i]) for i in range(n_x)]
 
     # warmup, all stages profiled to find the dominant kernel
-    all_stages = [qmoe.STAGE_ROUTER, qmoe.STAGE_SELECT, qmoe.STAGE_GATE_UP, qmoe.STAGE_DOWN, qmoe.STAGE_FUSED]
+    all_stages = list(range(qmoe.STAGE_COUNT))
     for L in layers:
         L.profile_enable(all_stages)
         L.profile_read(reset=True)
@@ -198,6 +273,9 @@ def main():
     dom_avg_s = dom_ms / 1e3 / max(dom_n, 1)
     dom_bytes = float(np.mean([per_x_bytes[s % n_x][dom] for s in range(args.steps)]))
     achieved = dom_bytes / dom_avg_s / 1e9
+    mfma_path = layers[0].forward_path(T) == qmoe.PATH_MFMA
+    dom_flops = stage_flops(cfg, T).get(dom, 0) if mfma_path else 0
+    mfma_tflops = dom_flops / dom_avg_s / 1e12
 
     # whole-layer roofline: all algorithmic bytes / measured step time
     def layer_step_bytes(bmap):
@@ -219,7 +297,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16" if mfma_path else "f32",
         "data": "synthetic",
         "config": {
             "workload": desc, "tokens_per_step": T, "hidden": cfg.hidden, "n_experts": cfg.n_experts,
@@ -227,17 +305,26 @@ def main():
             "select_scope": scope, "router_fmt": qmoe.FORMAT_NAMES[cfg.router_fmt],
             "expert_fmt": qmoe.FORMAT_NAMES[cfg.expert_fmt], "weight_copies": copies,
             "weight_bytes_per_copy": layer_total, "x_pool": n_x, "seed": args.seed,
+            "path": "mfma" if mfma_path else "gemv",
         },
         "roofline": {
             "bound": "hbm", "kernel": qmoe.STAGE_NAMES[dom], "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None, "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_avg_s * 1e6, 3),
         },
+        "mfma": ({"kernel": qmoe.STAGE_NAMES[dom], "flops_per_launch": int(dom_flops),
+                  "achieved_tflops": round(mfma_tflops, 1), "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                  "util": round(mfma_tflops / MFMA_BF16_PEAK_TFLOPS, 4)} if mfma_path else None),
         "layer_roofline": {
             "bytes_per_step": int(layer_bytes_step), "achieved_gbs": round(layer_gbs, 1),
             "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "stage_avg_us": stage_avg_us,
         },
     }
+    if skew:
+        result["config"]["skew"] = {"target_max_over_median": skew["target_max_over_median"],
+                                    "c": skew["per_x"][0]["c"], "max_load": skew["per_x"][0]["max_load"],
+                                    "median_load": skew["per_x"][0]["median_load"],
+                                    "experts_used": skew["per_x"][0]["experts_used"]}
     if not args.no_cpu_baseline:
         scope_for_oracle = scope
         result["cpu_baseline"] = cpu_baseline(hw, cfg, T, scope_for_oracle, xs_host, args.cpu_seconds)

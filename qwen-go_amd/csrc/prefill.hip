@@ -36,10 +36,9 @@ namespace qmoe {
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
 
-constexpr int kBM = 128;        // slots per tile
+constexpr int kBM = 256;        // slots per tile
 constexpr int kBK = 64;         // K per stage (128 bytes of bf16 per row)
-constexpr int kGemmThreads = 256;
-constexpr int kStageBytes = 2 * kBM * kBK * 2;  // A (128 x 64) + B (128 x 64) bf16
+constexpr int kGemmThreads = 512;
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -48,15 +47,29 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 }
 
 // LDS byte offset of the 16-byte chunk c (of 8 k values) of row r in a
-// 128-byte-row tile, XOR-swizzled by the row.
-__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// 128-byte-row tile, XOR-swizzled by the row.  The LDS has 64 banks (256
+// bytes) and serves a 16-byte-per-lane read 16 lanes at a time; those lanes
+// read 16 consecutive rows at one logical chunk, and (r >> 1) & 7 spreads each
+// pair of rows sharing a 256-byte bank line over distinct chunks.
+__device__ __forceinline__ int swz_of(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_of(r)) << 4); }
 
-__device__ __forceinline__ void dma16(const void *src, unsigned char *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
+// LDS offset of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
-// s_waitcnt vmcnt(0), other counters untouched.
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+// 16 bytes per lane from global memory straight into LDS at lds_wave_base +
+// 16 * lane (lds_wave_base is wave-uniform).  Issued through asm so that the
+// compiler does not track these loads: the GEMM waits for them explicitly
+// (wait_vm), and loads the compiler does track that were issued later only make
+// its own waits more conservative, never insufficient.
+__device__ __forceinline__ void dma16(const void *src, const unsigned char *lds_wave_base) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds_wave_base));
+  // one wait state between the M0 write and the LDS-direct load that reads it
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0)
+               : "memory", "m0");
+}
 
 // ------------------------------------------------------------------ prep
 
@@ -160,11 +173,11 @@ struct TileInfo {
   bool ok;
 };
 
-__device__ __forceinline__ TileInfo tile_of(const PrefillPlan &p, int E, bool shared_launch) {
+__device__ __forceinline__ TileInfo tile_of(const PrefillPlan &p, int E, bool shared_launch, int tile) {
   TileInfo ti{0, 0, 0, false};
   const int nt = shared_launch ? p.n_tiles[1] : p.n_tiles[0];
-  if ((int)blockIdx.x >= nt) return ti;
-  const int idx = shared_launch ? p.n_tiles[0] + blockIdx.x : blockIdx.x;
+  if (tile >= nt) return ti;
+  const int idx = shared_launch ? p.n_tiles[0] + tile : tile;
   ti.g = p.tile_grp[idx];
   const int m0 = p.tile_m0[idx];
   ti.slot0 = p.grp_off[ti.g] + m0;
@@ -173,154 +186,115 @@ __device__ __forceinline__ TileInfo tile_of(const PrefillPlan &p, int E, bool sh
   return ti;
 }
 
-// --------------------------------------------------------------- gate_up
+// ----------------------------------------------------------- grouped GEMM
+//
+// One workgroup: 256 slots x 128 output columns, 8 waves; wave w owns slots
+// [64 (w & 3), +64) and half of the columns (w >> 2).  K advances 64 at a time
+// through a ring of 3 LDS stages filled by global_load_lds two steps ahead.
+//   A stage: 256 rows x 128 bytes (bf16 rows of x, or of act), chunk-swizzled.
+//   B stage (gate_up): 128 weight rows x 128 bytes -- gate rows [n0, n0+64)
+//            then up rows [I+n0, I+n0+64) -- chunk-swizzled like A.
+//   B stage (down):    64 K rows x 256 bytes of the (I, H) down matrix
+//            (128 columns); a lane gathers its 8 K values of one column with
+//            8 two-byte LDS reads.  Chunks are XOR-ed with 4 in K rows 8..15
+//            of every 16 so that the two half-waves hit different banks.
 
-// Output block 128 slots x (64 gate + 64 up) columns.  Wave w: slots
-// [64 (w & 1), +64), gate/up columns [32 (w >> 1), +32) -- the gate and up
-// accumulators of a lane hold the same (slot, column), so SwiGLU is local.
-__global__ void __launch_bounds__(kGemmThreads) gemm_gate_up_bf16(PrefillArgs a, int shared_launch) {
-  const TileInfo ti = tile_of(a.p, a.E, shared_launch);
-  if (!ti.ok) return;
-  const bool sh = ti.g == a.E;
-  const int N = sh ? a.Is : a.I;
-  const int n0 = blockIdx.y * 64;
-  if (n0 >= N) return;
-  const int H = a.H;
-  extern __shared__ __align__(16) unsigned char lds[];
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+enum GemmKind { kGateUp = 0, kDown = 1 };
 
-  // rows this thread stages: A rows / B rows ((i * 4 + w) * 8 + lane / 8)
-  const uint16_t *arow[4], *brow[4];
-  const uint8_t *gbase = sh ? a.sgate : a.gu + (size_t)ti.g * a.gu_bytes;
-  const uint8_t *ubase = sh ? a.sup : gbase + (size_t)a.I * H * 2;
-  int chunk[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r = (i * 4 + w) * 8 + (lane >> 3);
-    chunk[i] = (lane & 7) ^ (r & 7);
-    const int m = min(r, ti.rows - 1);
-    arow[i] = a.xb + (size_t)a.p.tok[ti.slot0 + m] * H;
-    brow[i] = reinterpret_cast<const uint16_t *>(r < 64 ? gbase + (size_t)(n0 + r) * H * 2
-                                                        : ubase + (size_t)(n0 + r - 64) * H * 2);
-  }
-  auto issue = [&](int stage, int k0) {
-    unsigned char *sa = lds + stage * kStageBytes, *sb = sa + kBM * 128;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      dma16(arow[i] + k0 + chunk[i] * 8, sa + (i * 4 + w) * 1024);
-      dma16(brow[i] + k0 + chunk[i] * 8, sb + (i * 4 + w) * 1024);
-    }
-  };
+constexpr int kWaves = kGemmThreads / 64;
+constexpr int kNStage = 3;
+constexpr int kAStage = kBM * kBK * 2;          // 32 KB
+constexpr int kBStage = 128 * kBK * 2;          // 16 KB
+constexpr int kStage = kAStage + kBStage;
+constexpr int kADma = kAStage / 16 / kGemmThreads;  // 16-byte pieces per thread per stage
+constexpr int kBDma = kBStage / 16 / kGemmThreads;
 
-  const int wm = w & 1, wn = w >> 1;
-  f32x16_t acc[2][2];  // [m block][gate, up]
-#pragma unroll
-  for (int b = 0; b < 2; b++)
-#pragma unroll
-    for (int q = 0; q < 2; q++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[b][q][e] = 0.0f;
-
-  const int KT = H / kBK;
-  issue(0, 0);
-  const int ar0 = wm * 64 + (lane & 31), br0 = wn * 32 + (lane & 31), hi = lane >> 5;
-  for (int kt = 0; kt < KT; kt++) {
-    wait_vm0();
-    __syncthreads();  // stage kt landed everywhere; stage kt + 1 is free
-    const unsigned char *sa = lds + (kt & 1) * kStageBytes, *sb = sa + kBM * 128;
-    bf16x8_t av[2][4], bv[2][4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-      const int c = ks * 2 + hi;
-#pragma unroll
-      for (int b = 0; b < 2; b++) av[b][ks] = *reinterpret_cast<const bf16x8_t *>(sa + swz(ar0 + 32 * b, c));
-      bv[0][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(br0, c));
-      bv[1][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(64 + br0, c));
-    }
-    if (kt + 1 < KT) issue((kt + 1) & 1, (kt + 1) * kBK);
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-      for (int b = 0; b < 2; b++)
-#pragma unroll
-        for (int q = 0; q < 2; q++)
-          acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b][ks], bv[q][ks], acc[b][q], 0, 0, 0);
-  }
-  // epilogue: act = silu(g) * u -> bf16, row pitch Imax
-  const int n = n0 + wn * 32 + (lane & 31);
-#pragma unroll
-  for (int b = 0; b < 2; b++)
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = wm * 64 + b * 32 + 8 * j + 4 * hi + i;
-        if (m < ti.rows) {
-          const float g = acc[b][0][4 * j + i], u = acc[b][1][4 * j + i];
-          const float s = g / (1.0f + __expf(-g));
-          a.act[(size_t)(ti.slot0 + m) * a.Imax + n] = f32_to_bf16_rne(s * u);
-        }
-      }
+// s_waitcnt vmcnt(N) with the other counters untouched (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
 }
 
-// ------------------------------------------------------------------ down
+// Workgroup barrier for the GEMM pipeline.  __syncthreads() also waits for
+// every outstanding global load (vmcnt(0)), which would drain the prefetched
+// stages.  Here each wave has already waited for its own LDS-direct loads of
+// the stage (wait_vm) and for its LDS reads of the previous stage (consumed by
+// its MFMAs), so the bare s_barrier suffices; the empty asm statements keep the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
-// Output block 128 slots x 128 hidden columns.  Wave w: slots
-// [64 (w & 1), +64), columns [64 (w >> 1), +64).  The down matrix is stored
-// (I, H), N-contiguous: each thread loads 4 K rows x 8 columns (4 x 16 bytes),
-// transposes them in registers and writes 8 column-rows of 4 K values.
-__global__ void __launch_bounds__(kGemmThreads) gemm_down_bf16(PrefillArgs a, int shared_launch) {
-  const TileInfo ti = tile_of(a.p, a.E, shared_launch);
+// Work order, XCD-aware: workgroups are dealt to the 8 XCDs round-robin by
+// linear id, so id -> (tile, column chunk) gives every XCD whole tiles and runs
+// the ny column chunks of a tile back to back on one XCD, whose L2 then holds
+// the tile's A rows (gathered x, or act) for all of them.
+constexpr int kXcds = 8;
+
+template <int KIND>
+__global__ void __launch_bounds__(kGemmThreads) grouped_gemm_bf16(PrefillArgs a, int shared_launch, int ny) {
+  __shared__ __align__(16) unsigned char lds0[kStage], lds1[kStage], lds2[kStage];
+  const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+  const int tile = (j / ny) * kXcds + xcd, chunk = j % ny;
+  const TileInfo ti = tile_of(a.p, a.E, shared_launch, tile);
   if (!ti.ok) return;
   const bool sh = ti.g == a.E;
-  const int K = sh ? a.Is : a.I;
   const int H = a.H;
-  const int n0 = blockIdx.y * 128;
-  extern __shared__ __align__(16) unsigned char lds[];
+  const int N = KIND == kGateUp ? (sh ? a.Is : a.I) : H;       // output columns of the group
+  const int K = KIND == kGateUp ? H : (sh ? a.Is : a.I);
+  const int n0 = chunk * (KIND == kGateUp ? 64 : 128);
+  if (n0 >= N) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
 
-  const uint16_t *arow[4];
-  int chunk[4];
+  // A rows staged by this thread: row r = (i * kWaves + w) * 8 + lane / 8
+  const uint16_t *arow[kADma];
+  int achunk[kADma];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r = (i * 4 + w) * 8 + (lane >> 3);
-    chunk[i] = (lane & 7) ^ (r & 7);
-    arow[i] = a.act + (size_t)(ti.slot0 + min(r, ti.rows - 1)) * a.Imax;
+  for (int i = 0; i < kADma; i++) {
+    const int r = (i * kWaves + w) * 8 + (lane >> 3);
+    achunk[i] = (lane & 7) ^ swz_of(r);
+    const int m = min(r, ti.rows - 1);
+    if constexpr (KIND == kGateUp) arow[i] = a.xb + (size_t)a.p.tok[ti.slot0 + m] * H;
+    else arow[i] = a.act + (size_t)(ti.slot0 + m) * a.Imax;
   }
-  const uint16_t *dbase = reinterpret_cast<const uint16_t *>(sh ? a.sdown : a.dn + (size_t)ti.g * a.dn_bytes);
-  const int kq = tid >> 4, nc = tid & 15;  // this thread's 4 K rows and 8 columns of the B tile
-  const uint16_t *bsrc = dbase + (size_t)(4 * kq) * H + n0 + 8 * nc;
-  uint4 breg[4];
-  auto load_b = [&](int k0) {
+  // B pieces staged by this thread
+  const uint16_t *bsrc[kBDma];
 #pragma unroll
-    for (int r = 0; r < 4; r++) breg[r] = *reinterpret_cast<const uint4 *>(bsrc + (size_t)(k0 + r) * H);
-  };
-  auto store_b = [&](int stage) {
-    unsigned char *sb = lds + stage * kStageBytes + kBM * 128;
-    const uint32_t in[4][4] = {{breg[0].x, breg[0].y, breg[0].z, breg[0].w},
-                               {breg[1].x, breg[1].y, breg[1].z, breg[1].w},
-                               {breg[2].x, breg[2].y, breg[2].z, breg[2].w},
-                               {breg[3].x, breg[3].y, breg[3].z, breg[3].w}};
+  for (int i = 0; i < kBDma; i++) {
+    const int sidx = (i * kWaves + w) * 64 + lane;  // 16-byte slot of the stage
+    if constexpr (KIND == kGateUp) {
+      const int r = sidx >> 3, c = (sidx & 7) ^ swz_of(r);
+      const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)ti.g * a.gu_bytes;
+      const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * H * 2;
+      const uint8_t *row = r < 64 ? gb + (size_t)(n0 + r) * H * 2 : ub + (size_t)(n0 + r - 64) * H * 2;
+      bsrc[i] = reinterpret_cast<const uint16_t *>(row) + c * 8;
+    } else {
+      const int kr = sidx >> 4, c = (sidx & 15) ^ (((kr >> 3) & 1) << 2);
+      const uint8_t *db = sh ? a.sdown : a.dn + (size_t)ti.g * a.dn_bytes;
+      bsrc[i] = reinterpret_cast<const uint16_t *>(db) + (size_t)kr * H + n0 + c * 8;
+    }
+  }
+  auto issue = [&](unsigned char *sa, int k0) {
+    unsigned char *sb = sa + kAStage;
 #pragma unroll
-    for (int d = 0; d < 4; d++) {
-      // columns 2d (low halves) and 2d + 1 (high halves) of the 4 K rows
-      const uint32_t lo01 = __builtin_amdgcn_perm(in[1][d], in[0][d], 0x05040100u);
-      const uint32_t lo23 = __builtin_amdgcn_perm(in[3][d], in[2][d], 0x05040100u);
-      const uint32_t hi01 = __builtin_amdgcn_perm(in[1][d], in[0][d], 0x07060302u);
-      const uint32_t hi23 = __builtin_amdgcn_perm(in[3][d], in[2][d], 0x07060302u);
-      const int r0 = 8 * nc + 2 * d, r1 = r0 + 1;
-      *reinterpret_cast<uint2 *>(sb + swz(r0, kq >> 1) + (kq & 1) * 8) = make_uint2(lo01, lo23);
-      *reinterpret_cast<uint2 *>(sb + swz(r1, kq >> 1) + (kq & 1) * 8) = make_uint2(hi01, hi23);
+    for (int i = 0; i < kADma; i++) dma16(arow[i] + k0 + achunk[i] * 8, sa + (i * kWaves + w) * 1024);
+#pragma unroll
+    for (int i = 0; i < kBDma; i++) {
+      const uint16_t *src = KIND == kGateUp ? bsrc[i] + k0 : bsrc[i] + (size_t)k0 * H;
+      dma16(src, sb + (i * kWaves + w) * 1024);
     }
   };
-  auto issue_a = [&](int stage, int k0) {
-    unsigned char *sa = lds + stage * kStageBytes;
-#pragma unroll
-    for (int i = 0; i < 4; i++) dma16(arow[i] + k0 + chunk[i] * 8, sa + (i * 4 + w) * 1024);
-  };
 
-  const int wm = w & 1, wn = w >> 1;
-  f32x16_t acc[2][2];  // [m block][n block]
+  // wave w: slot rows [64 (w >> 1), +64), column half w & 1.  The SIMD of
+  // wave w also runs wave w + 4, whose rows lie 128 further: a tile with few
+  // rows still keeps every SIMD's MFMA busy, and 32-row blocks past the tile's
+  // rows skip their LDS reads and MFMAs.
+  const int wm = w >> 1, wn = w & 1, hi = lane >> 5, l32 = lane & 31;
+  const int nb = min(2, max(0, (ti.rows - wm * 64 + 31) >> 5));  // live 32-row blocks of this wave
+  f32x16_t acc[2][2];  // [slot block][gate/up, or column block]
 #pragma unroll
   for (int b = 0; b < 2; b++)
 #pragma unroll
@@ -329,58 +303,97 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_down_bf16(PrefillArgs a, in
       for (int e = 0; e < 16; e++) acc[b][q][e] = 0.0f;
 
   const int KT = K / kBK;
-  issue_a(0, 0);
-  load_b(0);
-  wait_vm0();
-  store_b(0);
-  const int ar0 = wm * 64 + (lane & 31), br0 = wn * 64 + (lane & 31), hi = lane >> 5;
-  for (int kt = 0; kt < KT; kt++) {
-    __syncthreads();  // stage kt complete (A by DMA, B by stores); stage kt + 1 free
-    const unsigned char *sa = lds + (kt & 1) * kStageBytes, *sb = sa + kBM * 128;
+  const int ar0 = wm * 64 + l32;
+  // one K step on stage `cur`; refills stage `nxt2` with step kt + 2
+  // Every step issues one batch of loads, so that the count of loads in flight
+  // is the same at every step: past the end of K the batch re-reads the last K
+  // slice into a stage that is never read again.
+  auto step = [&](const unsigned char *cur, unsigned char *nxt2, int kt) {
+    wait_vm<kADma + kBDma>();  // stage kt landed; the batch of step kt + 1 may still fly
+    lds_barrier();             // stage kt visible to all; stage kt + 2 (read at kt - 1) is free
+    const unsigned char *sa = cur, *sb = cur + kAStage;
     bf16x8_t av[2][4], bv[2][4];
+    if (nb == 0) {  // nothing to multiply: keep the pipeline's loads in step
+      issue(nxt2, min(kt + 2, KT - 1) * kBK);
+      return;
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
       const int c = ks * 2 + hi;
 #pragma unroll
-      for (int b = 0; b < 2; b++) {
-        av[b][ks] = *reinterpret_cast<const bf16x8_t *>(sa + swz(ar0 + 32 * b, c));
-        bv[b][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(br0 + 32 * b, c));
+      for (int b = 0; b < 2; b++)
+        if (b < nb) av[b][ks] = *reinterpret_cast<const bf16x8_t *>(sa + swz(ar0 + 32 * b, c));
+      if constexpr (KIND == kGateUp) {
+        bv[0][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(wn * 32 + l32, c));
+        bv[1][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(64 + wn * 32 + l32, c));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          const int nl = wn * 64 + q * 32 + l32;
+          const unsigned char *col = sb + (((nl >> 3) ^ (hi << 2)) << 4) + (nl & 7) * 2 + (ks * 16 + hi * 8) * 256;
+          union {
+            uint16_t h[8];
+            bf16x8_t v;
+          } u;
+#pragma unroll
+          for (int i = 0; i < 8; i++) u.h[i] = *reinterpret_cast<const uint16_t *>(col + i * 256);
+          bv[q][ks] = u.v;
+        }
       }
     }
-    if (kt + 1 < KT) {
-      issue_a((kt + 1) & 1, (kt + 1) * kBK);
-      load_b((kt + 1) * kBK);
-    }
+    issue(nxt2, min(kt + 2, KT - 1) * kBK);
 #pragma unroll
     for (int ks = 0; ks < 4; ks++)
 #pragma unroll
       for (int b = 0; b < 2; b++)
+        if (b < nb)
 #pragma unroll
-        for (int q = 0; q < 2; q++)
-          acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b][ks], bv[q][ks], acc[b][q], 0, 0, 0);
-    if (kt + 1 < KT) {
-      wait_vm0();
-      store_b((kt + 1) & 1);
-    }
+          for (int q = 0; q < 2; q++)
+            acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b][ks], bv[q][ks], acc[b][q], 0, 0, 0);
+  };
+  issue(lds0, 0);
+  issue(lds1, min(1, KT - 1) * kBK);
+  for (int kt = 0; kt < KT; kt += 3) {
+    step(lds0, lds2, kt);
+    if (kt + 1 < KT) step(lds1, lds0, kt + 1);
+    if (kt + 2 < KT) step(lds2, lds1, kt + 2);
   }
-  // epilogue: y[slot] = w_slot * acc, f32
+  wait_vm<0>();  // no LDS-direct load may land after the workgroup ends
+
+  if constexpr (KIND == kGateUp) {
+    // act = silu(g) * u -> bf16 (model/moe.go:64-75), row pitch Imax
+    const int n = n0 + wn * 32 + l32;
 #pragma unroll
-  for (int b = 0; b < 2; b++)
+    for (int b = 0; b < 2; b++)
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+      for (int j = 0; j < 4; j++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = wm * 64 + b * 32 + 8 * j + 4 * hi + i;
-        if (m < ti.rows) {
-          const int slot = ti.slot0 + m;
-          const float ws = a.p.wslot[slot];
-#pragma unroll
-          for (int q = 0; q < 2; q++) {
-            const int n = n0 + wn * 64 + q * 32 + (lane & 31);
-            a.y[(size_t)slot * H + n] = ws * acc[b][q][4 * j + i];
+        for (int i = 0; i < 4; i++) {
+          const int m = wm * 64 + b * 32 + 8 * j + 4 * hi + i;
+          if (m < ti.rows) {
+            const float g = acc[b][0][4 * j + i], u = acc[b][1][4 * j + i];
+            const float sgl = g / (1.0f + __expf(-g));
+            a.act[(size_t)(ti.slot0 + m) * a.Imax + n] = f32_to_bf16_rne(sgl * u);
           }
         }
-      }
+  } else {
+    // y[slot] = routing weight (or shared gate) * (down . act), f32
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int m = wm * 64 + b * 32 + 8 * j + 4 * hi + i;
+          if (m < ti.rows) {
+            const int slot = ti.slot0 + m;
+            const float ws = a.p.wslot[slot];
+#pragma unroll
+            for (int q = 0; q < 2; q++)
+              a.y[(size_t)slot * H + n0 + wn * 64 + q * 32 + l32] = ws * acc[b][q][4 * j + i];
+          }
+        }
+  }
 }
 
 // --------------------------------------------------------------- combine
@@ -433,18 +446,20 @@ hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, con
   return hipGetLastError();
 }
 
-hipError_t launch_prefill_gate_up(const PrefillArgs &a, bool shared, hipStream_t st) {
+template <int KIND>
+static hipError_t gemm_launch(const PrefillArgs &a, bool shared, int ny, hipStream_t st) {
   const int tiles = shared ? (a.T + kBM - 1) / kBM : prefill_max_tiles(a.T, a.k, a.E);
-  const int ny = (shared ? a.Is : a.I) / 64;
-  hipLaunchKernelGGL(gemm_gate_up_bf16, dim3(tiles, ny), dim3(kGemmThreads), 2 * kStageBytes, st, a, (int)shared);
+  const int blocks = (tiles + kXcds - 1) / kXcds * kXcds * ny;
+  hipLaunchKernelGGL(grouped_gemm_bf16<KIND>, dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny);
   return hipGetLastError();
 }
 
+hipError_t launch_prefill_gate_up(const PrefillArgs &a, bool shared, hipStream_t st) {
+  return gemm_launch<kGateUp>(a, shared, (shared ? a.Is : a.I) / 64, st);
+}
+
 hipError_t launch_prefill_down(const PrefillArgs &a, bool shared, hipStream_t st) {
-  const int tiles = shared ? (a.T + kBM - 1) / kBM : prefill_max_tiles(a.T, a.k, a.E);
-  hipLaunchKernelGGL(gemm_down_bf16, dim3(tiles, a.H / 128), dim3(kGemmThreads), 2 * kStageBytes, st, a,
-                     (int)shared);
-  return hipGetLastError();
+  return gemm_launch<kDown>(a, shared, a.H / 128, st);
 }
 
 hipError_t launch_prefill_combine(const PrefillArgs &a, float *out, hipStream_t st) {

@@ -62,18 +62,20 @@ __global__ void __launch_bounds__(64) router_rowwise_kernel(const float *__restr
 }
 
 // Register-tiled SIMT product for many tokens: a 256-thread block computes a
-// 64-token x 64-expert tile, 4x4 outputs per thread, staging 32-wide k slices
-// of x and of the router in LDS.  Every output still sums its products in h
-// order, so the result equals the row-wise kernel's bit for bit.
+// 32-token x 32-expert tile, 2 x 2 outputs per thread (tokens ty, ty + 16 and
+// experts tx, tx + 16), staging 32-wide k slices of x and of the router in LDS
+// with k contiguous.  Small tiles keep every SIMD busy: the work is one
+// dependent f32 add chain of length H per output.  Every output still sums its
+// products in h order, so the result equals the row-wise kernel's bit for bit.
 template <int FMT>
 __global__ void __launch_bounds__(256) router_tiled_kernel(const float *__restrict__ x, int T, int H,
                                                            const uint8_t *__restrict__ w,
                                                            const uint16_t *__restrict__ s, int E,
                                                            float *__restrict__ logits) {
 #pragma clang fp contract(off)
-  constexpr int KB = 32, TM = 64, TN = 64, PAD = 4;
-  __shared__ __align__(16) float xs[KB][TM + PAD];
-  __shared__ __align__(16) float ws[KB][TN + PAD];
+  constexpr int KB = 32, TM = 32, TN = 32, LD = KB + 4;
+  __shared__ __align__(16) float xs[TM][LD];
+  __shared__ __align__(16) float ws[TN][LD];
   const int tid = threadIdx.x;
   const int tx = tid & 15, ty = tid >> 4;
   const int t0 = blockIdx.y * TM, e0 = blockIdx.x * TN;
@@ -82,60 +84,91 @@ __global__ void __launch_bounds__(256) router_tiled_kernel(const float *__restri
   const int64_t row_bytes = fmt_matrix_bytes(FMT, 1, H);
   const int nsc = H / kGroup;
 
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
-
-  for (int k0 = 0; k0 < H; k0 += KB) {
-    // x slice: TM rows x 32 floats, 8 float4 per row.
-    for (int i = tid; i < TM * (KB / 4); i += 256) {
-      int r = i / (KB / 4), c4 = i % (KB / 4);
-      int t = t0 + r;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (t < T) v = *reinterpret_cast<const float4 *>(x + (size_t)t * H + k0 + c4 * 4);
-      xs[c4 * 4 + 0][r] = v.x;
-      xs[c4 * 4 + 1][r] = v.y;
-      xs[c4 * 4 + 2][r] = v.z;
-      xs[c4 * 4 + 3][r] = v.w;
+  static_assert(TN * CPR <= 256, "one router chunk per thread and slice");
+  // this thread's share of a slice: one float4 of x, at most one 16-byte
+  // router chunk; the next slice is loaded raw into registers while the
+  // current one is multiplied, and widened once it is stored
+  const int xr = tid >> 3, xc4 = tid & 7;
+  const bool x_ok = t0 + xr < T;
+  const float *xsrc = x + (size_t)min(t0 + xr, T - 1) * H + xc4 * 4;
+  const int wr = tid / CPR, wc = tid % CPR;
+  const bool w_ok = tid < TN * CPR && e0 + wr < E;
+  const uint8_t *wrow = w + (size_t)min(e0 + wr, E - 1) * row_bytes;
+  const uint16_t *wsrow = fmt_quant(FMT) ? s + (size_t)min(e0 + wr, E - 1) * nsc : nullptr;
+  float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
+  uint4 wraw = make_uint4(0u, 0u, 0u, 0u);
+  uint16_t wsc = 0;
+  auto load_slice = [&](int k0) {
+    if (x_ok) xv = *reinterpret_cast<const float4 *>(xsrc + k0);
+    if (w_ok) {
+      const int chunk = k0 / EPC + wc;
+      wraw = *reinterpret_cast<const uint4 *>(wrow + (size_t)chunk * 16);
+      if constexpr (fmt_quant(FMT)) wsc = wsrow[(chunk * EPC) / kGroup];
     }
-    // router slice: TN rows x 32 elements, widened to f32.
-    for (int i = tid; i < TN * CPR; i += 256) {
-      int r = i / CPR, c = i % CPR;
-      int e = e0 + r;
+  };
+
+  float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+  load_slice(0);
+  for (int k0 = 0; k0 < H; k0 += KB) {
+    *reinterpret_cast<float4 *>(&xs[xr][xc4 * 4]) = xv;
+    if (tid < TN * CPR) {  // widen the router chunk exactly as router_chunk does
       float wv[EPC];
-      if (e < E) {
-        router_chunk<FMT>(w + (size_t)e * row_bytes, fmt_quant(FMT) ? s + (size_t)e * nsc : nullptr,
-                          k0 / EPC + c, wv);
-      } else {
+      const uint32_t u[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
+      if constexpr (FMT == kF32) {
 #pragma unroll
-        for (int q = 0; q < EPC; q++) wv[q] = 0.0f;
+        for (int i = 0; i < 4; i++) wv[i] = __uint_as_float(u[i]);
+      } else if constexpr (FMT == kBF16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          wv[2 * i] = __uint_as_float(u[i] << 16);
+          wv[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+        }
+      } else if constexpr (FMT == kINT8) {
+        const float sc = f16_to_f32(wsc);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int b = 0; b < 4; b++) wv[4 * i + b] = (float)(int8_t)((u[i] >> (8 * b)) & 0xffu) * sc;
+      } else {
+        const float sc = f16_to_f32(wsc);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int b = 0; b < 4; b++) {
+            const uint32_t byte = (u[i] >> (8 * b)) & 0xffu;
+            wv[8 * i + 2 * b] = (float)((int)(byte >> 4) - 8) * sc;
+            wv[8 * i + 2 * b + 1] = (float)((int)(byte & 0xfu) - 8) * sc;
+          }
       }
 #pragma unroll
-      for (int q = 0; q < EPC; q++) ws[c * EPC + q][r] = wv[q];
+      for (int q = 0; q < EPC; q++) ws[wr][wc * EPC + q] = w_ok ? wv[q] : 0.0f;
     }
     __syncthreads();
-#pragma unroll 4
-    for (int kk = 0; kk < KB; kk++) {
-      float4 a = *reinterpret_cast<const float4 *>(&xs[kk][ty * 4]);
-      float4 b = *reinterpret_cast<const float4 *>(&ws[kk][tx * 4]);
-      const float av[4] = {a.x, a.y, a.z, a.w};
-      const float bv[4] = {b.x, b.y, b.z, b.w};
+    if (k0 + KB < H) load_slice(k0 + KB);
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+    for (int kk = 0; kk < KB; kk += 4) {
+      const float4 a0 = *reinterpret_cast<const float4 *>(&xs[ty][kk]);
+      const float4 a1 = *reinterpret_cast<const float4 *>(&xs[ty + 16][kk]);
+      const float4 b0 = *reinterpret_cast<const float4 *>(&ws[tx][kk]);
+      const float4 b1 = *reinterpret_cast<const float4 *>(&ws[tx + 16][kk]);
+      const float av[2][4] = {{a0.x, a0.y, a0.z, a0.w}, {a1.x, a1.y, a1.z, a1.w}};
+      const float bv[2][4] = {{b0.x, b0.y, b0.z, b0.w}, {b1.x, b1.y, b1.z, b1.w}};
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = acc[i][j] + av[i] * bv[j];
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+          for (int j = 0; j < 2; j++) acc[i][j] = acc[i][j] + av[i][q] * bv[j][q];
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    int t = t0 + ty * 4 + i;
+  for (int i = 0; i < 2; i++) {
+    const int t = t0 + ty + 16 * i;
     if (t >= T) continue;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      int e = e0 + tx * 4 + j;
+    for (int j = 0; j < 2; j++) {
+      const int e = e0 + tx + 16 * j;
       if (e < E) logits[(size_t)t * E + e] = acc[i][j];
     }
   }
@@ -150,7 +183,7 @@ static hipError_t router_logits_fmt(const float *x, int T, const DevMat &r, floa
     hipLaunchKernelGGL(router_rowwise_kernel<FMT>, grid, dim3(64), (size_t)H * sizeof(float), st, x,
                        T, H, r.w, r.s, E, logits);
   } else {
-    dim3 grid((E + 63) / 64, (T + 63) / 64);
+    dim3 grid((E + 31) / 32, (T + 31) / 32);
     hipLaunchKernelGGL(router_tiled_kernel<FMT>, grid, dim3(256), 0, st, x, T, H, r.w, r.s, E,
                        logits);
   }

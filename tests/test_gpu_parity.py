@@ -7,8 +7,9 @@ Bars (written into each assertion):
     whose weights come from f64 logits within its rounding bound of the
     reference's f32 logits; the exact path matches to the last bit of exp);
   * dequantised weights and device-quantised codes/scales: bit-exact;
-  * layer output on the GEMV path (f32 activations): normwise relative error
-    max_j|y-y_ref| / max_j|y_ref| <= 1e-3 per token.
+  * layer output, normwise relative error max_j|y-y_ref| / max_j|y_ref| per
+    token: <= 1e-3 on the decode (GEMV) path, f32 activations; <= 2e-2 on the
+    batched MFMA path (x and the SwiGLU output in bf16, f32 accumulation).
 Every test prints the case it runs before touching the GPU.
 """
 import numpy as np
@@ -30,11 +31,20 @@ def announce(msg):
     print(f"[case] {msg}", flush=True)
 
 
-def check_layer(cfg, hw, x, tol=TOL_F32, scope=None):
+TOL_MFMA = 2e-2  # batched path: x and the SwiGLU output rounded to bf16, f32 accumulation
+
+
+def path_tol(layer, T):
+    """The parity bar of the kernels the library runs for T tokens."""
+    return TOL_MFMA if layer.forward_path(T) == qmoe.PATH_MFMA else TOL_F32
+
+
+def check_layer(cfg, hw, x, tol=None, scope=None):
     layer = qmoe.MoeLayer(cfg)
     try:
         hw.upload(layer)
         out, ids, w = layer.forward(x)
+        tol = tol or path_tol(layer, x.shape[0])
     finally:
         layer.close()
     ref, rids, rw = oracle.OracleLayer(hw, scope=scope).forward(x)
@@ -204,13 +214,14 @@ def test_router_exact_ties(T):
         hw.upload(layer)
         out, ids, w = layer.forward(x)
         fb = layer.router_fallbacks()
+        tol = path_tol(layer, T)
     finally:
         layer.close()
     ref, rids, rw = oracle.OracleLayer(hw).forward(x)
     assert np.array_equal(ids, rids), (ids, rids)
     # the leading ranks are a tied group, listed in ascending index order
     assert list(ids[0][:2]) in ([3, 5], [2, 9]), ids[0]
-    assert rel_err(out, ref) <= TOL_F32
+    assert rel_err(out, ref) <= tol
     if T <= 32:
         assert fb >= T  # every token hit a tie
 
@@ -242,8 +253,6 @@ def test_golden_tiny_layer(scope_tag):
 
 
 # ------------------------------------------------- batched (MFMA) path
-
-TOL_MFMA = 2e-2  # x and the SwiGLU output rounded to bf16, f32 accumulation
 
 
 def check_mfma_layer(cfg, hw, x, scope=None):
