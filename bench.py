@@ -61,7 +61,36 @@ def parse():
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--skew", type=float, default=10.0,
                     help="prefill: target ratio of the busiest expert's load to the median load")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB, 5 times (the calibration "
+                         "kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE), and exit")
     return ap.parse_args()
+
+
+def copy_probe(mib):
+    """A plain copy kernel of known size: reads and writes mib MiB per launch."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": n * 4, "launches": 5}))
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary for this workload (profiles/traffic_<workload>.txt: FETCH_SIZE and
+    WRITE_SIZE, each scaled by the copy kernel's calibration), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) >= 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+            return int(float(parts[2]))
+    return None
 
 
 # prefill workloads: router weights x4 and tokens pulled along one direction
@@ -176,6 +205,9 @@ def cpu_baseline(hw, cfg, T, scope, xs, budget_s):
 
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               f"(the MoE block is built and measured on a single MI355X)", file=sys.stderr)
@@ -310,7 +342,8 @@ def main():
         "roofline": {
             "bound": "hbm", "kernel": qmoe.STAGE_NAMES[dom], "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None, "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_avg_s * 1e6, 3),
+            "traffic": measured_traffic(args.workload, qmoe.STAGE_NAMES[dom]),
+            "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_avg_s * 1e6, 3),
         },
         "mfma": ({"kernel": qmoe.STAGE_NAMES[dom], "flops_per_launch": int(dom_flops),
                   "achieved_tflops": round(mfma_tflops, 1), "peak_tflops": MFMA_BF16_PEAK_TFLOPS,

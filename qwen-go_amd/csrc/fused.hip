@@ -497,7 +497,7 @@ static void fused_launch(const FusedArgs &a0, hipStream_t st) {
       return;  // the error stays set; launch_expert_fused reports it
     allowed = lds;
   }
-  hipLaunchKernelGGL((expert_fused_kernel<FMT, ITER, NJ>), dim3(blocks), dim3(kFusedBlock), lds, st, a);
+  QMOE_LAUNCH((expert_fused_kernel<FMT, ITER, NJ>), dim3(blocks), dim3(kFusedBlock), lds, st, a);
 }
 
 template <int FMT, int ITER>
@@ -540,7 +540,7 @@ __global__ void __launch_bounds__(256) zero_kernel(float *__restrict__ p, int64_
 
 hipError_t launch_zero(float *p, int64_t n, hipStream_t st) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, st, p, n);
+  QMOE_LAUNCH(zero_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, st, p, n);
   return hipGetLastError();
 }
 

@@ -2,10 +2,32 @@
 // between the kernel translation units and the C ABI in layer.hip).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace qmoe {
+
+// Kernel timing for qmoe_profile_*: while a stage is profiled, the layer sets
+// these to an event pair; the stage's launches then go through
+// hipExtLaunchKernelGGL, which records `start` when its first kernel starts and
+// `stop` when its last kernel ends -- the kernels' own execution time, without
+// the dispatch gap that events recorded around the launch would add.
+struct ProfEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local ProfEvents g_prof;
+
+#define QMOE_LAUNCH(kernel, grid, block, lds, st, ...)                                              \
+  do {                                                                                             \
+    if (::qmoe::g_prof.stop) {                                                                     \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, st, ::qmoe::g_prof.start, ::qmoe::g_prof.stop, \
+                            0, __VA_ARGS__);                                                       \
+      ::qmoe::g_prof.start = nullptr;                                                              \
+    } else {                                                                                       \
+      hipLaunchKernelGGL(kernel, grid, block, lds, st, __VA_ARGS__);                               \
+    }                                                                                              \
+  } while (0)
 
 // One stored weight matrix (or a stack of them) on the device.
 struct DevMat {

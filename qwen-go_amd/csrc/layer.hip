@@ -79,6 +79,10 @@ struct qmoe_layer {
   int64_t prof_calls[QMOE_STAGE_COUNT] = {};
 };
 
+namespace qmoe {
+thread_local ProfEvents g_prof;
+}
+
 namespace {
 
 qmoe_status fail(qmoe_layer *l, qmoe_status s, const std::string &msg) {
@@ -226,13 +230,12 @@ hipError_t next_event(qmoe_layer *l, hipEvent_t *ev) {
     if (_on) {                                                                \
       HIP_TRY(l, next_event(l, &_a), "hipEventCreate");                       \
       HIP_TRY(l, next_event(l, &_b), "hipEventCreate");                       \
-      HIP_TRY(l, hipEventRecord(_a, st), "hipEventRecord");                   \
+      g_prof = ProfEvents{_a, _b};                                            \
     }                                                                         \
-    HIP_TRY(l, expr, what);                                                   \
-    if (_on) {                                                                \
-      HIP_TRY(l, hipEventRecord(_b, st), "hipEventRecord");                   \
-      (l)->recs.push_back({(sid), _a, _b});                                   \
-    }                                                                         \
+    const hipError_t _se = (expr);                                            \
+    g_prof = ProfEvents{};                                                    \
+    if (_se != hipSuccess) return hip_fail(l, _se, what);                     \
+    if (_on) (l)->recs.push_back({(sid), _a, _b});                            \
   } while (0)
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }

@@ -439,9 +439,9 @@ int prefill_max_tiles(int T, int k, int E) {
 hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, const float *wts, const float *x,
                                    const float *shared_gate, float *sg, hipStream_t st) {
   const bool with_shared = a.Is > 0;
-  hipLaunchKernelGGL(prep_kernel, dim3(a.T), dim3(256), 0, st, x, a.H, with_shared ? shared_gate : nullptr, a.xb,
+  QMOE_LAUNCH(prep_kernel, dim3(a.T), dim3(256), 0, st, x, a.H, with_shared ? shared_gate : nullptr, a.xb,
                      sg);
-  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, st, ids, wts, sg, a.T, a.k, a.E,
+  QMOE_LAUNCH(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, st, ids, wts, sg, a.T, a.k, a.E,
                      (int)with_shared, a.p);
   return hipGetLastError();
 }
@@ -450,7 +450,7 @@ template <int KIND>
 static hipError_t gemm_launch(const PrefillArgs &a, bool shared, int ny, hipStream_t st) {
   const int tiles = shared ? (a.T + kBM - 1) / kBM : prefill_max_tiles(a.T, a.k, a.E);
   const int blocks = (tiles + kXcds - 1) / kXcds * kXcds * ny;
-  hipLaunchKernelGGL(grouped_gemm_bf16<KIND>, dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny);
+  QMOE_LAUNCH(grouped_gemm_bf16<KIND>, dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny);
   return hipGetLastError();
 }
 
@@ -463,7 +463,7 @@ hipError_t launch_prefill_down(const PrefillArgs &a, bool shared, hipStream_t st
 }
 
 hipError_t launch_prefill_combine(const PrefillArgs &a, float *out, hipStream_t st) {
-  hipLaunchKernelGGL(combine_kernel, dim3(a.T), dim3(256), 0, st, a.y, a.p.slot_of, a.T, a.k, a.H,
+  QMOE_LAUNCH(combine_kernel, dim3(a.T), dim3(256), 0, st, a.y, a.p.slot_of, a.T, a.k, a.H,
                      (int)(a.Is > 0), out);
   return hipGetLastError();
 }

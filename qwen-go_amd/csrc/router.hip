@@ -180,11 +180,11 @@ static hipError_t router_logits_fmt(const float *x, int T, const DevMat &r, floa
   const int H = r.cols, E = r.rows;
   if (T <= 32) {
     dim3 grid((E + 63) / 64, T);
-    hipLaunchKernelGGL(router_rowwise_kernel<FMT>, grid, dim3(64), (size_t)H * sizeof(float), st, x,
+    QMOE_LAUNCH(router_rowwise_kernel<FMT>, grid, dim3(64), (size_t)H * sizeof(float), st, x,
                        T, H, r.w, r.s, E, logits);
   } else {
     dim3 grid((E + 31) / 32, (T + 31) / 32);
-    hipLaunchKernelGGL(router_tiled_kernel<FMT>, grid, dim3(256), 0, st, x, T, H, r.w, r.s, E,
+    QMOE_LAUNCH(router_tiled_kernel<FMT>, grid, dim3(256), 0, st, x, T, H, r.w, r.s, E,
                        logits);
   }
   return hipGetLastError();
@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(64) softmax_select_kernel(const float *__restr
 
 hipError_t launch_softmax_select(const float *logits, int T, int E, int k, int scope, int32_t *ids,
                                  float *weights, hipStream_t st) {
-#define L(NJ) hipLaunchKernelGGL(softmax_select_kernel<NJ>, dim3(T), dim3(64), 0, st, logits, E, k, scope, ids, weights)
+#define L(NJ) QMOE_LAUNCH(softmax_select_kernel<NJ>, dim3(T), dim3(64), 0, st, logits, E, k, scope, ids, weights)
   QMOE_NJ_DISPATCH(E, L);
 #undef L
   return hipGetLastError();
@@ -312,7 +312,7 @@ static bool sb_fmt(const float *x, int T, const DevMat &r, double *sb, float *ze
   const int H = r.cols, E = r.rows;
   const int cpl = (H / EPC + 63) / 64;
   dim3 grid((E + 3) / 4, T);
-#define L(C) hipLaunchKernelGGL((router_sb_kernel<FMT, C>), grid, dim3(256), 0, st, x, H, r.w, r.s, E, sb, zero_out)
+#define L(C) QMOE_LAUNCH((router_sb_kernel<FMT, C>), grid, dim3(256), 0, st, x, H, r.w, r.s, E, sb, zero_out)
   // at most 64 products per lane (H <= 4096)
   switch (cpl) {
   case 1: L(1); return true;
@@ -376,7 +376,7 @@ size_t select_cert_lds_bytes(int E, int H) { return (size_t)H * 4 + (size_t)E * 
 hipError_t launch_select_cert(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
                               int32_t *ids, float *weights, unsigned int *fallbacks, hipStream_t st) {
   const size_t lds = select_cert_lds_bytes(router.rows, router.cols);
-#define L(NJ) hipLaunchKernelGGL(select_cert_kernel<NJ>, dim3(T), dim3(256), lds, st, x, router, k, scope, sb, ids, \
+#define L(NJ) QMOE_LAUNCH(select_cert_kernel<NJ>, dim3(T), dim3(256), lds, st, x, router, k, scope, sb, ids, \
                                weights, fallbacks)
   QMOE_NJ_DISPATCH(router.rows, L);
 #undef L
