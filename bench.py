@@ -353,6 +353,10 @@ def main():
             "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "stage_avg_us": stage_avg_us,
         },
     }
+    fb = sum(L.router_fallbacks() for L in layers)
+    result["layer_roofline"]["router_fallbacks"] = {
+        "tokens": int(fb), "of_tokens": int(T * (n_x + args.warmup + args.steps)),
+        "note": "tokens the certified decode router could not certify (recomputed exactly)"}
     if skew:
         result["config"]["skew"] = {"target_max_over_median": skew["target_max_over_median"],
                                     "c": skew["per_x"][0]["c"], "max_load": skew["per_x"][0]["max_load"],

@@ -39,6 +39,23 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
   return h;
 }
 
+// LDS offset of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// 16 bytes per lane from global memory straight into LDS at lds_wave_base +
+// 16 * lane (lds_wave_base is wave-uniform).  Issued through asm so that the
+// compiler does not track these loads: the GEMM waits for them explicitly
+// (wait_vm), and loads the compiler does track that were issued later only make
+// its own waits more conservative, never insufficient.
+__device__ __forceinline__ void dma16(const void *src, const unsigned char *lds_wave_base) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds_wave_base));
+  // one wait state between the M0 write and the LDS-direct load that reads it
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0)
+               : "memory", "m0");
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64);
 // every lane of the group receives the sum.
 __device__ __forceinline__ float group_sum(float v, int width) {

@@ -1,92 +1,55 @@
-// fused.hip -- the expert products for one forward in a single kernel.
+// fused.hip -- the expert products of a decode-sized forward in one kernel.
 //
-// Block = (token t, rank r, chunk c of 32 intermediate rows); a launch covers
-// the routed ranks, the shared expert (model/moe.go:86-97), or both.  One
-// control wave and eight data waves:
-//   control: picks the block's expert.  From the router partials it runs the
-//            certified selection (select.hpp): as soon as the round of rank r
-//            ends it publishes that tentative expert through LDS, then
-//            finishes the remaining rounds and the certification while the
-//            data waves stream.  With precomputed routing it just reads it.
-//            For the shared expert it computes sigmoid(shared_gate . x).
-//   data:    issue every load of the block at once -- gate and up rows
-//            [32c, 32c+32) of the expert into registers, and rows [32c, 32c+32)
-//            of its down matrix, stored transposed (I, H) so that they are one
-//            contiguous region, straight into LDS (global_load_lds) -- then
-//            compute act = silu(g) * u (model/moe.go:64-75) and
-//            w_r * (down[:, 32c:32c+32] . act), added into out[t] with f32
-//            atomics (model/moe.go:76-84).
-// The certification result is checked before any atomic; if the final expert
-// differs from the tentative one, the block recomputes with the final one.
-// When certification fails the whole block computes the exact sequential
-// logits of the token (the reference's bits) and selects on them.
-// Splitting the intermediate dimension across blocks removes the dependency
-// between the gate_up and the down products, so the layer needs no second
-// launch and no in-kernel handoff between blocks.  out must be zero on entry.
-// The atomics make the order of the final f32 sums run-dependent (within f32
-// rounding of the reference's rank-ordered sum).
-//
-// Work to blocks, XCD-aware: workgroups go to the 8 XCDs round-robin by linear
-// id; the chunks of one expert are given ids that spread evenly over them.
+// Each token's k * I routed intermediate rows (plus the Is rows of the shared
+// expert, model/moe.go:86-97) are split evenly over about one block per CU; a
+// block holds at most two runs of rows (a run = consecutive rows of one expert).
+// Eight waves; wave 0 is also the control wave:
+//   control: the certified selection from the router partials (select.hpp):
+//            after the round of rank r it publishes that rank's tentative expert
+//            in LDS, then finishes the rounds, certifies the order and computes
+//            the renormalised weights while the data waves stream.  With
+//            precomputed routing it just reads it.  For a shared-expert run it
+//            computes the scalar gate sigmoid(sharedGate . x).
+//   all:     each lane group owns a contiguous range of the block's rows and
+//            streams, two rows ahead, each row's gate and up rows and its row of
+//            the transposed (I, H) down matrix into registers; per row it forms
+//            act = silu(g) * u in f32 (model/moe.go:64-75) and accumulates
+//            act * down_row in registers, flushing the sum into the run's LDS
+//            accumulator (f32 LDS atomics) when the run -- or, for the group-32
+//            formats, the 32-row scale group -- changes.
+// The routing weight (or the shared gate) multiplies a run's accumulator once,
+// at the end, so the data waves can start on the tentative experts before the
+// weights are known; a run whose final expert differs from the tentative one
+// is recomputed.  When certification fails the whole block computes the
+// token's exact sequential logits and selects on them.  The block's result is
+// added into out with f32 atomics (model/moe.go:76-84); out must be zero on
+// entry.  The atomics make the order of the final f32 sums run-dependent
+// (within f32 rounding of the reference's rank-ordered sum).
 #include "gemv_common.hpp"
 #include "select.hpp"
 
 namespace qmoe {
 
-constexpr int kCtl = 64;                      // control wave
-constexpr int kData = 448;                    // data threads (7 waves)
-constexpr int kFusedBlock = kCtl + kData;
+constexpr int kCtl = 64;                      // control wave (wave 0)
+constexpr int kFusedBlock = 512;              // every wave, the control wave included, streams rows
+constexpr int kData = kFusedBlock;
 constexpr int kMaxRows = 192;                 // intermediate rows per block, at most
-constexpr int kDownLds = 128 * 1024;          // LDS bytes for down-slice staging
-constexpr int kMaxRowsPerGroup = 4;
 
-// Rows per lane group whose loads are in flight together: as many as fit the
-// register budget of 512-thread blocks (the quantised dot products unpack
-// more per chunk).
-// Output chunks per data thread in the down product: two where a row of the
-// hidden size can have more 16-byte chunks than there are data threads.
-template <int FMT>
-constexpr int kDownPasses = FMT == kINT4 ? 1 : 2;
-
-template <int FMT, int ITER>
-constexpr int rows_in_flight() {
-  return (FMT == kINT4 && ITER >= 4) ? 1 : (fmt_quant(FMT) && ITER >= 4) ? 2 : kMaxRowsPerGroup;
+// LDS: x, two run accumulators, exact logits (fallback); then, for the burst
+// mode, each data wave's down rows (kBurstKB KiB per wave).
+constexpr int kBurstKB = 16;
+__host__ __device__ inline size_t fused_head_bytes(int H, int E) {
+  return ((size_t)(3 * H + E) * 4 + 15) / 16 * 16;
 }
-
-// Rows of the transposed down slice staged per LDS pass.
-template <int FMT>
-__host__ __device__ inline int stage_rows(int H) {
-  const int64_t row = fmt_matrix_bytes(FMT, 1, H);
-  int r = (int)(kDownLds / row);
-  return r >= 32 ? 32 : (r >= 16 ? 16 : (r >= 8 ? 8 : 0));
-}
-template <int FMT>
+constexpr size_t kLdsLimit = 160 * 1024 - 2048;  // static LDS < 1 KiB
+__host__ inline size_t fused_burst_bytes() { return (size_t)(kData / 64) * kBurstKB * 1024; }
+__host__ inline bool fused_burst_fits(int H, int E) { return fused_head_bytes(H, E) + fused_burst_bytes() <= kLdsLimit; }
 __host__ inline size_t fused_lds_bytes(int H, int E) {
-  const size_t head = ((size_t)(H + kMaxRows + E) * 4 + 15) / 16 * 16;
-  // stage_slice writes whole passes of kData x 16 bytes
-  const size_t pass = (size_t)kData * 16;
-  const size_t slice = ((size_t)stage_rows<FMT>(H) * fmt_matrix_bytes(FMT, 1, H) + pass - 1) / pass * pass;
-  const int epc = Chunk<FMT>::kElems;
-  const int jc = H / epc;
-  const int ig = jc >= kData ? 1 : kData / jc;
-  const size_t part = (size_t)ig * H * 4;
-  return head + (slice > part ? slice : part);
+  return fused_head_bytes(H, E) + (fused_burst_fits(H, E) ? fused_burst_bytes() : 0);
 }
 
-// Issues the loads of `rows` contiguous stored down rows (each row_bytes) into
-// dsl (LDS), 16 bytes per data lane per instruction.
-__device__ __forceinline__ void stage_slice(const uint8_t *__restrict__ src, int64_t bytes, unsigned char *dsl,
-                                            int dt) {
-  const int64_t n16 = bytes / 16;
-  for (int64_t p = 0; p * kData < n16; p++) {
-    int64_t q = p * kData + dt;
-    q = q < n16 ? q : n16 - 1;  // the tail reloads a valid piece that is never used
-    auto *dst = (__attribute__((address_space(3))) void *)(dsl + ((size_t)p * kData + (dt & ~63)) * 16);
-    __builtin_amdgcn_global_load_lds(src + q * 16, dst, 16, 0, 0);
-  }
-}
-
-// acc[0..EPC) += a * w for one 16-byte chunk of stored weights.
+// acc[0..EPC) += a * w for one 16-byte chunk of stored weights (INT formats:
+// the raw codes; the group scale is applied when the sum is flushed).
 template <int FMT>
 __device__ __forceinline__ void chunk_axpy(const uint4 v, float a, float (&acc)[Chunk<FMT>::kElems]) {
   const uint32_t u[4] = {v.x, v.y, v.z, v.w};
@@ -116,39 +79,30 @@ __device__ __forceinline__ void chunk_axpy(const uint4 v, float a, float (&acc)[
   }
 }
 
-// acc[q] += (a * sc[q]) * w[q]: one chunk of a quantised row whose group
-// scales differ per output.
-template <int FMT>
-__device__ __forceinline__ void chunk_axpy_scaled(const uint4 v, float a, const float (&sc)[Chunk<FMT>::kElems],
-                                                  float (&acc)[Chunk<FMT>::kElems]) {
-  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-  if constexpr (FMT == kINT8) {
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-      for (int b = 0; b < 4; b++)
-        acc[4 * q + b] = fmaf(a * sc[4 * q + b], (float)(int8_t)((u[q] >> (8 * b)) & 0xffu), acc[4 * q + b]);
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-      for (int b = 0; b < 4; b++) {
-        const uint32_t byte = (u[q] >> (8 * b)) & 0xffu;
-        acc[8 * q + 2 * b] = fmaf(a * sc[8 * q + 2 * b], (float)((int)(byte >> 4) - 8), acc[8 * q + 2 * b]);
-        acc[8 * q + 2 * b + 1] = fmaf(a * sc[8 * q + 2 * b + 1], (float)((int)(byte & 0xfu) - 8), acc[8 * q + 2 * b + 1]);
-      }
-  }
+// Rows whose loads are in flight per lane group: two while they fit the
+// register budget of a 512-thread block.
+template <int ITER>
+constexpr int prefetch_rows() {
+  return ITER > 0 && ITER <= 4 ? 2 : 1;
 }
-
-// One intermediate row of the block: which expert it belongs to and where.
-struct RowRef {
-  int seg;  // 0 or 1: the block's first or second run of rows
-  int i;    // intermediate index within the expert
-};
+// Burst mode: a lane group (one wave) owning at most this many rows issues all
+// of them at once -- gate and up rows into registers, down rows into the wave's
+// LDS region -- so the whole block's data is in flight together.
+template <int FMT, int ITER>
+constexpr int burst_rows() {
+  return ITER <= 0 ? 0 : ITER * Chunk<FMT>::kElems > 32 ? 2 : (kBurstKB / ITER < 4 ? kBurstKB / ITER : 4);
+}
+// Up to 32 outputs per lane the row sums stay in registers between flushes;
+// wider rows add each row's products straight into the LDS run sums.
+template <int FMT, int ITER>
+constexpr bool accumulate_in_registers() {
+  return ITER > 0 && ITER * Chunk<FMT>::kElems <= 32;
+}
 
 template <int FMT, int ITER, int NJ>
 __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) {
   constexpr int EPC = Chunk<FMT>::kElems;
+  constexpr int IT = ITER > 0 ? ITER : 1;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_ids[64];
   __shared__ float s_w[64];
@@ -158,9 +112,9 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   __shared__ int s_xready;  // data waves whose share of x is in LDS
   const int H = a.H;
   float *xs = reinterpret_cast<float *>(smem);
-  float *act = xs + H;                      // kMaxRows (act scaled by the routing weight)
-  float *lt = act + kMaxRows;
-  unsigned char *dsl = smem + ((size_t)(H + kMaxRows + a.E) * 4 + 15) / 16 * 16;
+  float *red = xs + H;        // (2, H): the block's two runs
+  float *lt = red + 2 * H;    // exact logits (fallback)
+  unsigned char *burst_lds = smem + fused_head_bytes(H, a.E);
 
   // ---- block -> (token, rows [u0, u1) of the token's flattened rows)
   const int t = blockIdx.x / a.nb;
@@ -194,146 +148,334 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   const int nruns = n1 > 0 ? 2 : 1;
   auto run_rank = [&](int q) { return q ? rank1 : rank0; };
   const bool ctl = threadIdx.x < kCtl;
-  const int dt = threadIdx.x - kCtl;
+  const int dt = threadIdx.x;  // row-streaming thread index (all threads)
   const bool writer = blockIdx.x % a.nb == 0 && a.sb && a.k_routed > 0;
 
-  if (threadIdx.x < 64) s_spec[threadIdx.x] = a.sb ? 0 : 1;
+  if (threadIdx.x < 64) s_spec[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_xready = 0;
+  for (int j = threadIdx.x; j < 2 * H; j += kFusedBlock) red[j] = 0.0f;
   __syncthreads();
-  // The data waves load x[t] into LDS and count themselves done in s_xready;
-  // the control wave starts the selection at once, without x.
+  // Waves 1..7 load x[t] into LDS and count themselves done in s_xready; the
+  // control wave starts the selection at once, without x.
   if (!ctl) {
-    for (int i = dt * 4; i < H; i += kData * 4)
+    for (int i = (threadIdx.x - kCtl) * 4; i < H; i += (kFusedBlock - kCtl) * 4)
       *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.x + (size_t)t * H + i);
-    if ((dt & 63) == 0) __hip_atomic_fetch_add(&s_xready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if ((threadIdx.x & 63) == 0)
+      __hip_atomic_fetch_add(&s_xready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   auto wait_x = [&]() {
-    while (__hip_atomic_load(&s_xready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < kData / 64)
+    while (__hip_atomic_load(&s_xready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < (kFusedBlock - kCtl) / 64)
       __builtin_amdgcn_s_sleep(1);
   };
 
-  // ---- geometry
+  // ---- geometry of a row: nch 16-byte chunks, lpr lanes per row
   const int64_t row_bytes = fmt_matrix_bytes(FMT, 1, H);  // gate/up rows and transposed down rows
   const int gnsc = H / kGroup;
   const int nch = H / EPC;
+  // The run sums are stored element-major: output j = ch * EPC + e sits at
+  // e * nch + ch, so a lane-parallel update of element e of each lane's chunk
+  // touches consecutive words (no LDS bank conflicts).
+  auto pos = [&](int ch, int e) { return e * nch + ch; };
   const int lpr = lanes_per_row(nch);
   const int groups = kData / lpr;
   const int g = dt / lpr, sl = dt % lpr;
-  const int SR = stage_rows<FMT>(H);
+  const int rs = (int)((int64_t)g * nrows / groups), re = (int)((int64_t)(g + 1) * nrows / groups);
+  // burst mode (block-uniform): every lane group is one wave with at most
+  // burst_rows rows, and the LDS holds the burst regions
+  const bool use_burst = a.burst && lpr == 64 && (nrows + groups - 1) / groups <= burst_rows<FMT, ITER>() &&
+                         2 * H * 4 <= kBurstKB * 1024;
 
-  // expert of run q (tentative for data waves until certification ends)
+  // expert of run q: tentative (published in s_spec, for the data waves) or
+  // final (s_ids); both live in LDS in either routing mode
   auto run_expert = [&](int q, bool tentative) -> int {
     const int rk = run_rank(q);
     if (rk == a.k) return 0;
-    if (!a.sb) return a.ids[(size_t)t * a.k + rk];
     return tentative ? s_spec[rk] - 1 : s_ids[rk];
   };
-  auto gate_ptr = [&](int q, int e, int i, const uint8_t *&gr, const uint8_t *&ur, const uint16_t *&gsr,
-                      const uint16_t *&usr) {
-    const bool sh = run_rank(q) == a.k;
-    const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)e * a.gu_bytes;
-    const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * row_bytes;
-    gr = gb + (size_t)i * row_bytes;
-    ur = ub + (size_t)i * row_bytes;
-    gsr = usr = nullptr;
-    if constexpr (fmt_quant(FMT)) {
-      const uint16_t *gs = sh ? a.sgate_s : a.gu_s + (size_t)e * a.gu_scales;
-      const uint16_t *us = sh ? a.sup_s : gs + (size_t)a.I * gnsc;
-      gsr = gs + (size_t)i * gnsc;
-      usr = us + (size_t)i * gnsc;
-    }
-  };
-  auto down_row = [&](int q, int e, int i) -> const uint8_t * {
-    const bool sh = run_rank(q) == a.k;
-    return (sh ? a.sdown : a.dn + (size_t)e * a.dn_bytes) + (size_t)i * row_bytes;
-  };
-  auto down_scales = [&](int q, int e, int i) -> const uint16_t * {  // scale row of i's group
-    const bool sh = run_rank(q) == a.k;
-    return (sh ? a.sdown_s : a.dn_s + (size_t)e * a.dn_scales) + (size_t)(i / kGroup) * H;
-  };
-  auto row_of = [&](int rho) -> RowRef { return rho < n0 ? RowRef{0, i00 + rho} : RowRef{1, i01 + rho - n0}; };
 
-  // Stage rows [r0, r0 + n) of the block's rows (down, transposed) into LDS.
-  auto stage = [&](int r0, int n, int e0, int e1) {
-    const int per_row = (int)(row_bytes / 16);
-    const int total = n * per_row;
-    for (int p = 0; p * kData < total; p++) {
-      int qd = p * kData + dt;
-      qd = qd < total ? qd : total - 1;  // the tail reloads a valid piece that is never used
-      const RowRef rr = row_of(r0 + qd / per_row);
-      const uint8_t *src = down_row(rr.seg, rr.seg ? e1 : e0, rr.i) + (size_t)(qd % per_row) * 16;
-      auto *dst = (__attribute__((address_space(3))) void *)(dsl + ((size_t)p * kData + (dt & ~63)) * 16);
-      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
-    }
-  };
-
-  // gate_up of the block's rows: act[rho] = silu(g) * u, loads in batches of
-  // kMaxRowsPerGroup rows per lane group, all issued before the dots.
-  auto gate_up = [&](int e0, int e1) {
-    constexpr int RIF = rows_in_flight<FMT, ITER>();
-    for (int b0 = g; b0 < nrows; b0 += RIF * groups) {
-      if constexpr (ITER > 0) {
-        uint4 vg[RIF][ITER], vu[RIF][ITER];
-        const uint16_t *sgp[RIF], *sup[RIF];
+  // Rows [rs, re) of this lane group for the runs in `mask`, experts e0/e1.
+  auto process_rows = [&](int e0_in, int e1_in, int mask, bool burst) {
+    const int e0 = __builtin_amdgcn_readfirstlane(e0_in), e1 = __builtin_amdgcn_readfirstlane(e1_in);
+    struct RowPtr {
+      const uint8_t *g, *u, *d;
+      const uint16_t *gs, *us, *ds;  // INT: gate/up scale rows; down scale row of the 32-row group
+      int q, grp;
+    };
+    auto row_ptr = [&](int rho) -> RowPtr {
+      RowPtr p;
+      p.q = rho < n0 ? 0 : 1;
+      const int i = p.q ? i01 + rho - n0 : i00 + rho;
+      const bool sh = run_rank(p.q) == a.k;
+      const int e = p.q ? e1 : e0;
+      const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)e * a.gu_bytes;
+      const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * row_bytes;
+      p.g = gb + (size_t)i * row_bytes;
+      p.u = ub + (size_t)i * row_bytes;
+      p.d = (sh ? a.sdown : a.dn + (size_t)e * a.dn_bytes) + (size_t)i * row_bytes;
+      p.grp = i / kGroup;
+      p.gs = p.us = p.ds = nullptr;
+      if constexpr (fmt_quant(FMT)) {
+        const uint16_t *gsb = sh ? a.sgate_s : a.gu_s + (size_t)e * a.gu_scales;
+        const uint16_t *usb = sh ? a.sup_s : gsb + (size_t)a.I * gnsc;
+        p.gs = gsb + (size_t)i * gnsc;
+        p.us = usb + (size_t)i * gnsc;
+        p.ds = (sh ? a.sdown_s : a.dn_s + (size_t)e * a.dn_scales) + (size_t)p.grp * H;
+      }
+      return p;
+    };
+    // per-lane running sum of act * down for the current (run, scale group)
+    constexpr bool kAcc = accumulate_in_registers<FMT, ITER>();
+    constexpr int AIT = kAcc ? IT : 1;
+    float acc[AIT][EPC];
 #pragma unroll
-        for (int qq = 0; qq < RIF; qq++) {
-          const int rho = b0 + qq * groups;
-          if (rho < nrows) {
-            const RowRef rr = row_of(rho);
-            const uint8_t *gr, *ur;
-            gate_ptr(rr.seg, rr.seg ? e1 : e0, rr.i, gr, ur, sgp[qq], sup[qq]);
+    for (int c = 0; c < AIT; c++)
 #pragma unroll
-            for (int c = 0; c < ITER; c++) {
-              vg[qq][c] = *reinterpret_cast<const uint4 *>(gr + (size_t)(sl + c * lpr) * 16);
-              vu[qq][c] = *reinterpret_cast<const uint4 *>(ur + (size_t)(sl + c * lpr) * 16);
+      for (int e = 0; e < EPC; e++) acc[c][e] = 0.0f;
+    int cur_q = -1, cur_grp = -1;
+    const uint16_t *cur_ds = nullptr;
+    auto flush = [&]() {
+      if (!kAcc || cur_q < 0) return;
+      float *rq = red + cur_q * H;
+#pragma unroll
+      for (int c = 0; c < AIT; c++) {
+        const int ch = sl + c * lpr;
+#pragma unroll
+        for (int e = 0; e < EPC; e++) {
+          float v = acc[c][e];
+          if constexpr (fmt_quant(FMT)) v *= f16_to_f32(cur_ds[ch * EPC + e]);
+          atomicAdd(rq + pos(ch, e), v);
+          acc[c][e] = 0.0f;
+        }
+      }
+    };
+    auto act_of = [&](float gv, float uv) {
+      gv = group_sum(gv, lpr);
+      uv = group_sum(uv, lpr);
+      return silu_ref(gv) * uv;
+    };
+    auto begin_row = [&](const RowPtr &p) {
+      const bool same = p.q == cur_q && (!fmt_quant(FMT) || p.grp == cur_grp);
+      if (!same) {
+        flush();
+        cur_q = p.q;
+        cur_grp = p.grp;
+        cur_ds = p.ds;
+      }
+    };
+    constexpr int BR = burst_rows<FMT, ITER>();
+    if constexpr (BR > 0) {
+      if (burst && mask == 3) {
+        // Burst: every row of this wave in flight at once -- down rows into the
+        // wave's LDS region, gate and up rows (and, for the group-32 formats,
+        // the row's down scales) into registers.  The per-run sums stay in
+        // registers and are stored, without atomics, into the same LDS region
+        // once the down rows have been consumed.  One lane group = one wave, so
+        // rows and experts are wave-uniform and the row bases scalar.
+        unsigned char *wl = burst_lds + (size_t)(dt >> 6) * kBurstKB * 1024;
+        constexpr int SV = fmt_quant(FMT) ? IT * EPC / 8 : 1;  // 16-byte pieces of a lane's fp16 down scales
+        uint4 bg[BR][IT], bu[BR][IT], bs[BR][SV];
+        RowPtr bp[BR];
+        const int n = __builtin_amdgcn_readfirstlane(re - rs);
+        const int rs_u = __builtin_amdgcn_readfirstlane(rs);
+#pragma unroll
+        for (int r = 0; r < BR; r++)  // every pointer first, then every load
+          if (r < n) bp[r] = row_ptr(rs_u + r);
+#pragma unroll
+        for (int r = 0; r < BR; r++) {
+          if (r < n) {
+#pragma unroll
+            for (int c = 0; c < IT; c++)
+              dma16(bp[r].d + (size_t)(sl + c * lpr) * 16, wl + (r * IT + c) * 1024);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < BR; r++) {
+          if (r < n) {
+#pragma unroll
+            for (int c = 0; c < IT; c++) {
+              const size_t off = (size_t)(sl + c * lpr) * 16;
+              bg[r][c] = *reinterpret_cast<const uint4 *>(bp[r].g + off);
+              bu[r][c] = *reinterpret_cast<const uint4 *>(bp[r].u + off);
+            }
+            if constexpr (fmt_quant(FMT)) {
+              // the lane's outputs: chunk c covers EPC consecutive outputs
+#pragma unroll
+              for (int v = 0; v < SV; v++) {
+                const int c = v / (EPC / 8), part = v % (EPC / 8);
+                bs[r][v] = *reinterpret_cast<const uint4 *>(bp[r].ds + (sl + c * lpr) * EPC + part * 8);
+              }
             }
           }
         }
         wait_x();
+        float act[BR];
 #pragma unroll
-        for (int qq = 0; qq < RIF; qq++) {
-          const int rho = b0 + qq * groups;
-          float gv = 0.0f, uv = 0.0f;
-          if (rho < nrows) {
+        for (int r = 0; r < BR; r++) {
+          act[r] = 0.0f;
+          if (r < n) {
+            float gv = 0.0f, uv = 0.0f;
 #pragma unroll
-            for (int c = 0; c < ITER; c++) {
+            for (int c = 0; c < IT; c++) {
               const int ch = sl + c * lpr;
-              float dg = chunk_dot<FMT>(vg[qq][c], xs + ch * EPC);
-              float du = chunk_dot<FMT>(vu[qq][c], xs + ch * EPC);
+              float dg = chunk_dot<FMT>(bg[r][c], xs + ch * EPC);
+              float du = chunk_dot<FMT>(bu[r][c], xs + ch * EPC);
               if constexpr (fmt_quant(FMT)) {
-                dg *= f16_to_f32(sgp[qq][(ch * EPC) / kGroup]);
-                du *= f16_to_f32(sup[qq][(ch * EPC) / kGroup]);
+                dg *= f16_to_f32(bp[r].gs[(ch * EPC) / kGroup]);
+                du *= f16_to_f32(bp[r].us[(ch * EPC) / kGroup]);
               }
               gv += dg;
               uv += du;
             }
+            act[r] = act_of(gv, uv);
           }
-          gv = group_sum(gv, lpr);
-          uv = group_sum(uv, lpr);
-          if (sl == 0 && rho < nrows) act[rho] = silu_ref(gv) * uv;
         }
-      } else {
-        wait_x();
-#pragma unroll 1
-        for (int qq = 0; qq < RIF; qq++) {
-          const int rho = b0 + qq * groups;
-          if (rho >= nrows) break;
-          const RowRef rr = row_of(rho);
-          const uint8_t *gr, *ur;
-          const uint16_t *gsr, *usr;
-          gate_ptr(rr.seg, rr.seg ? e1 : e0, rr.i, gr, ur, gsr, usr);
-          float gv = row_dot_rt<FMT>(gr, gsr, xs, sl, lpr, nch);
-          float uv = row_dot_rt<FMT>(ur, usr, xs, sl, lpr, nch);
-          gv = group_sum(gv, lpr);
-          uv = group_sum(uv, lpr);
-          if (sl == 0) act[rho] = silu_ref(gv) * uv;
+        __builtin_amdgcn_s_waitcnt(0);  // the down rows have landed in LDS
+        float acc0[IT][EPC], acc1[IT][EPC];
+#pragma unroll
+        for (int c = 0; c < IT; c++)
+#pragma unroll
+          for (int e = 0; e < EPC; e++) acc0[c][e] = acc1[c][e] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < BR; r++) {
+          if (r < n) {
+#pragma unroll
+            for (int c = 0; c < IT; c++) {
+              const uint4 v = *reinterpret_cast<const uint4 *>(wl + (r * IT + c) * 1024 + sl * 16);
+              float w[EPC];
+#pragma unroll
+              for (int e = 0; e < EPC; e++) w[e] = 0.0f;
+              chunk_axpy<FMT>(v, act[r], w);
+              if constexpr (fmt_quant(FMT)) {
+#pragma unroll
+                for (int e = 0; e < EPC; e++) {
+                  const int k = c * EPC + e;  // the lane's k-th output
+                  const uint32_t word = (&bs[r][k / 8].x)[(k % 8) / 2];
+                  w[e] *= f16_to_f32((uint16_t)((k & 1) ? (word >> 16) : (word & 0xffffu)));
+                }
+              }
+              if (bp[r].q == 0) {
+#pragma unroll
+                for (int e = 0; e < EPC; e++) acc0[c][e] += w[e];
+              } else {
+#pragma unroll
+                for (int e = 0; e < EPC; e++) acc1[c][e] += w[e];
+              }
+            }
+          }
+        }
+        // the wave's run sums, in output order, into its own region
+        float *part = reinterpret_cast<float *>(wl);
+#pragma unroll
+        for (int c = 0; c < IT; c++) {
+          const int j0 = (sl + c * lpr) * EPC;
+#pragma unroll
+          for (int e = 0; e < EPC; e += 4) {
+            *reinterpret_cast<float4 *>(part + j0 + e) =
+                make_float4(acc0[c][e], acc0[c][e + 1], acc0[c][e + 2], acc0[c][e + 3]);
+            *reinterpret_cast<float4 *>(part + H + j0 + e) =
+                make_float4(acc1[c][e], acc1[c][e + 1], acc1[c][e + 2], acc1[c][e + 3]);
+          }
+        }
+        return;
+      }
+    }
+    if constexpr (ITER > 0) {
+      constexpr int PD = prefetch_rows<ITER>();
+      struct RowData {
+        uint4 g[IT], u[IT], d[IT];
+      };
+      RowData buf[PD];
+      RowPtr ptr[PD];
+      auto load = [&](int slot, int rho) {
+        ptr[slot] = row_ptr(rho);
+#pragma unroll
+        for (int c = 0; c < IT; c++) {
+          const size_t off = (size_t)(sl + c * lpr) * 16;
+          buf[slot].g[c] = *reinterpret_cast<const uint4 *>(ptr[slot].g + off);
+          buf[slot].u[c] = *reinterpret_cast<const uint4 *>(ptr[slot].u + off);
+          buf[slot].d[c] = *reinterpret_cast<const uint4 *>(ptr[slot].d + off);
+        }
+      };
+      auto consume = [&](int slot) {
+        const RowPtr &p = ptr[slot];
+        float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+        for (int c = 0; c < IT; c++) {
+          const int ch = sl + c * lpr;
+          float dg = chunk_dot<FMT>(buf[slot].g[c], xs + ch * EPC);
+          float du = chunk_dot<FMT>(buf[slot].u[c], xs + ch * EPC);
+          if constexpr (fmt_quant(FMT)) {
+            dg *= f16_to_f32(p.gs[(ch * EPC) / kGroup]);
+            du *= f16_to_f32(p.us[(ch * EPC) / kGroup]);
+          }
+          gv += dg;
+          uv += du;
+        }
+        const float act = act_of(gv, uv);
+        if constexpr (kAcc) {
+          begin_row(p);
+#pragma unroll
+          for (int c = 0; c < IT; c++) chunk_axpy<FMT>(buf[slot].d[c], act, acc[AIT > 1 ? c : 0]);
+        } else {
+          float *rq = red + p.q * H;
+#pragma unroll
+          for (int c = 0; c < IT; c++) {
+            const int ch = sl + c * lpr;
+            float w[EPC];
+#pragma unroll
+            for (int e = 0; e < EPC; e++) w[e] = 0.0f;
+            chunk_axpy<FMT>(buf[slot].d[c], act, w);
+#pragma unroll
+            for (int e = 0; e < EPC; e++) {
+              float v = w[e];
+              if constexpr (fmt_quant(FMT)) v *= f16_to_f32(p.ds[ch * EPC + e]);
+              atomicAdd(rq + pos(ch, e), v);
+            }
+          }
+        }
+      };
+      // rows of runs outside `mask` are skipped (they are only loaded)
+      auto wanted = [&](int rho) { return (mask >> (rho < n0 ? 0 : 1)) & 1; };
+#pragma unroll
+      for (int s = 0; s < PD; s++)
+        if (rs + s < re) load(s, rs + s);
+      wait_x();
+      for (int rho = rs; rho < re; rho += PD) {
+#pragma unroll
+        for (int s = 0; s < PD; s++) {
+          if (rho + s < re) {
+            if (wanted(rho + s)) consume(s);
+            if (rho + s + PD < re) load(s, rho + s + PD);
+          }
+        }
+      }
+    } else {
+      wait_x();
+      for (int rho = rs; rho < re; rho++) {
+        if (!((mask >> (rho < n0 ? 0 : 1)) & 1)) continue;
+        const RowPtr p = row_ptr(rho);
+        const float act = act_of(row_dot_rt<FMT>(p.g, p.gs, xs, sl, lpr, nch),
+                                 row_dot_rt<FMT>(p.u, p.us, xs, sl, lpr, nch));
+        float *rq = red + p.q * H;
+        for (int c = sl; c < nch; c += lpr) {
+          float w[EPC];
+#pragma unroll
+          for (int e = 0; e < EPC; e++) w[e] = 0.0f;
+          chunk_axpy<FMT>(*reinterpret_cast<const uint4 *>(p.d + (size_t)c * 16), act, w);
+#pragma unroll
+          for (int e = 0; e < EPC; e++) {
+            float v = w[e];
+            if constexpr (fmt_quant(FMT)) v *= f16_to_f32(p.ds[c * EPC + e]);
+            atomicAdd(rq + pos(c, e), v);
+          }
         }
       }
     }
+    flush();
   };
 
   bool need_exact = false;
-  int te0 = 0, te1 = 0;  // tentative experts of the two runs (data waves)
+  int te0 = 0, te1 = 0;  // tentative experts of the two runs
   if (ctl) {
     // ---- control wave: routing; the shared gate for a shared run
     const bool has_routed = rank0 != a.k;
@@ -343,9 +485,11 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
                                               writer ? a.weights + (size_t)t * a.k : nullptr, s_ids, s_w, -2,
                                               s_spec);
       need_exact = !ok;
-    } else if (has_routed && threadIdx.x < a.k) {
-      s_ids[threadIdx.x] = a.ids[(size_t)t * a.k + threadIdx.x];
+    } else if (has_routed && threadIdx.x < a.k) {  // precomputed routing
+      const int id = a.ids[(size_t)t * a.k + threadIdx.x];
+      s_ids[threadIdx.x] = id;
       s_w[threadIdx.x] = a.weights[(size_t)t * a.k + threadIdx.x];
+      __hip_atomic_store(&s_spec[threadIdx.x], id + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     if ((nruns > 1 ? rank1 : rank0) == a.k) {
       wait_x();
@@ -354,21 +498,20 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
       sgv = group_sum(sgv, 64);
       if (threadIdx.x == 0) s_sg = 1.0f / (1.0f + (float)exp(-(double)sgv));
     }
-  } else {
-    // ---- data waves: wait for the tentative experts of the block's runs
-    for (int q = 0; q < nruns; q++) {
-      const int rk = run_rank(q);
-      if (rk == a.k || !a.sb) continue;
-      while (__hip_atomic_load(&s_spec[rk], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
-        __builtin_amdgcn_s_sleep(1);
-    }
-    te0 = run_expert(0, true);
-    te1 = nruns > 1 ? run_expert(1, true) : 0;
-    stage(0, min(SR, nrows), te0, te1);
-    gate_up(te0, te1);
   }
+  // ---- every wave: wait for the tentative experts of the block's runs (the
+  // control wave has published them already) and stream its rows
+  for (int q = 0; q < nruns; q++) {
+    const int rk = run_rank(q);
+    if (rk == a.k) continue;
+    while (__hip_atomic_load(&s_spec[rk], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+      __builtin_amdgcn_s_sleep(1);
+  }
+  te0 = run_expert(0, true);
+  te1 = nruns > 1 ? run_expert(1, true) : 0;
+  process_rows(te0, te1, 3, use_burst);
   if (threadIdx.x == 0) s_exact = need_exact;
-  __syncthreads();  // act, s_ids/s_w (when certified), s_sg, s_exact
+  __syncthreads();  // run sums, s_ids/s_w (when certified), s_sg, s_exact
   if (s_exact) {
     // certification failed: the whole block computes the exact routing
     exact_logits_block(xs, H, a.rw, a.rs, a.rfmt, a.E, lt, kFusedBlock);
@@ -382,96 +525,43 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   }
   const int e0 = run_expert(0, false);
   const int e1 = nruns > 1 ? run_expert(1, false) : 0;
-  // data waves recompute when a tentative expert was not the final one
-  const bool redo = a.sb && ((rank0 != a.k && e0 != s_spec[rank0] - 1) ||
-                             (nruns > 1 && rank1 != a.k && e1 != s_spec[rank1] - 1));
+  // runs whose tentative expert was not the final one are recomputed
+  int redo = 0;
+  if (rank0 != a.k && e0 != s_spec[rank0] - 1) redo |= 1;
+  if (nruns > 1 && rank1 != a.k && e1 != s_spec[rank1] - 1) redo |= 2;
   if (redo) {
-    if (!ctl) __builtin_amdgcn_s_waitcnt(0);  // earlier LDS-direct loads have landed
-    __syncthreads();
-    if (!ctl) {
-      stage(0, min(SR, nrows), e0, e1);
-      gate_up(e0, e1);
-    }
-    __syncthreads();
-  }
-  // fold the routing weight (or the shared gate) into act
-  for (int rho = threadIdx.x; rho < nrows; rho += kFusedBlock) {
-    const int rk = rho < n0 ? rank0 : rank1;
-    act[rho] *= rk == a.k ? s_sg : s_w[rk];
-  }
-
-  // ---- down: out[t, j] += sum_rho act[rho] * downT[row rho][j].  Thread
-  // (ig, jc) owns the outputs of chunk jc (and of chunk jc + kData when the
-  // row has more chunks than there are data threads) over rows ig, ig + IG, ...
-  constexpr int NP = kDownPasses<FMT>;
-  const int JC = nch;
-  const int IG = JC >= kData ? 1 : kData / JC;
-  const int jc = dt % JC, ig = dt / JC;  // threads with ig >= IG idle here
-  float acc[NP][EPC];
-#pragma unroll
-  for (int pp = 0; pp < NP; pp++)
-#pragma unroll
-    for (int q = 0; q < EPC; q++) acc[pp][q] = 0.0f;
-  for (int s0 = 0; s0 < nrows; s0 += SR) {
-    const int srows = min(SR, nrows - s0);
-    if (s0 > 0 && !ctl) stage(s0, srows, e0, e1);
-    if (!ctl) __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();  // the whole stage is in LDS (and act is scaled)
-    if (!ctl && ig < IG) {
-#pragma unroll
-      for (int pp = 0; pp < NP; pp++) {
-        const int jcp = jc + pp * kData;
-        if (jcp >= JC) break;
-        if constexpr (fmt_quant(FMT)) {
-          // per row: the scales of its (expert, 32-row group) for these outputs
-          int cur = -1;
-          float sc[EPC];
-          for (int i = ig; i < srows; i += IG) {
-            const RowRef rr = row_of(s0 + i);
-            const int key = rr.seg * 65536 + rr.i / kGroup;
-            if (key != cur) {
-              const uint16_t *sp = down_scales(rr.seg, rr.seg ? e1 : e0, rr.i) + jcp * EPC;
-#pragma unroll
-              for (int q = 0; q < EPC; q++) sc[q] = f16_to_f32(sp[q]);
-              cur = key;
-            }
-            const uint4 v = *reinterpret_cast<const uint4 *>(dsl + (size_t)i * row_bytes + (size_t)jcp * 16);
-            chunk_axpy_scaled<FMT>(v, act[s0 + i], sc, acc[pp]);
-          }
-        } else {
-          const unsigned char *col = dsl + (size_t)jcp * 16;
-          int i = ig;
-          for (; i + 3 * IG < srows; i += 4 * IG) {  // four LDS reads in flight
-            uint4 v[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = *reinterpret_cast<const uint4 *>(col + (size_t)(i + r * IG) * row_bytes);
-#pragma unroll
-            for (int r = 0; r < 4; r++) chunk_axpy<FMT>(v[r], act[s0 + i + r * IG], acc[pp]);
-          }
-          for (; i < srows; i += IG)
-            chunk_axpy<FMT>(*reinterpret_cast<const uint4 *>(col + (size_t)i * row_bytes), act[s0 + i], acc[pp]);
+    // recompute the runs in `redo` into red (streaming mode); their burst
+    // partial sums are dropped
+    for (int j = threadIdx.x; j < H; j += kFusedBlock) {
+      if (redo & 1) red[j] = 0.0f;
+      if (redo & 2) red[H + j] = 0.0f;
+      if (use_burst)
+        for (int w = 0; w < kFusedBlock / 64; w++) {
+          float *part = reinterpret_cast<float *>(burst_lds + (size_t)w * kBurstKB * 1024);
+          if (redo & 1) part[j] = 0.0f;
+          if (redo & 2) part[H + j] = 0.0f;
         }
-      }
     }
-    __syncthreads();  // before the next stage (or the partials) overwrite LDS
+    __syncthreads();
+    process_rows(e0, e1, redo, false);
+    __syncthreads();
   }
-  // combine the IG partial sums of each output through LDS, add to out
-  float *part = reinterpret_cast<float *>(dsl);
-  if (!ctl && ig < IG) {
-#pragma unroll
-    for (int pp = 0; pp < NP; pp++) {
-      const int jcp = jc + pp * kData;
-      if (jcp < JC) {
-#pragma unroll
-        for (int q = 0; q < EPC; q++) part[(size_t)ig * H + jcp * EPC + q] = acc[pp][q];
-      }
-    }
-  }
-  __syncthreads();
+  // ---- out[t] += w_run * run sum (the routing weight, or the shared gate)
+  const float w0 = rank0 == a.k ? s_sg : s_w[rank0];
+  const float w1 = nruns > 1 ? (rank1 == a.k ? s_sg : s_w[rank1]) : 0.0f;
   float *out_t = a.out + (size_t)t * H;
+  // output order: the global atomics of a wave then cover 256 contiguous bytes
   for (int j = threadIdx.x; j < H; j += kFusedBlock) {
-    float v = 0.0f;
-    for (int q = 0; q < IG; q++) v += part[(size_t)q * H + j];
+    const int pj = pos(j / EPC, j % EPC);
+    float s0 = red[pj], s1 = red[H + pj];
+    if (use_burst)  // burst sums are stored in output order
+      for (int w = 0; w < kFusedBlock / 64; w++) {
+        const float *part = reinterpret_cast<const float *>(burst_lds + (size_t)w * kBurstKB * 1024);
+        s0 += part[j];
+        s1 += part[H + j];
+      }
+    float v = w0 * s0;
+    if (nruns > 1) v = fmaf(w1, s1, v);
     atomicAdd(out_t + j, v);
   }
 }
@@ -487,8 +577,9 @@ static void fused_launch(const FusedArgs &a0, hipStream_t st) {
   nb = max(nb, (U + rmax - 1) / rmax);
   a.rb = (U + nb - 1) / nb;
   a.nb = (U + a.rb - 1) / a.rb;
+  a.burst = fused_burst_fits(a.H, a.E);
   const int blocks = a.T * a.nb;
-  const size_t lds = fused_lds_bytes<FMT>(a.H, a.E);
+  const size_t lds = fused_lds_bytes(a.H, a.E);
   // dynamic LDS above 64 KiB has to be allowed per kernel (once per size)
   static size_t allowed = 64 * 1024;
   if (lds > allowed) {
@@ -507,28 +598,33 @@ static void fused_nj(const FusedArgs &a, hipStream_t st) {
 #undef L
 }
 
+// Rows of more than 64 elements per lane take the run-time chunk loop (the
+// unrolled loads would not fit the registers).
+template <int FMT, int ITER>
+constexpr int usable_iter() {
+  return ITER * Chunk<FMT>::kElems > 64 ? 0 : ITER;
+}
+
+template <int FMT, int ITER>
+static void fused_iter(const FusedArgs &a, hipStream_t st) {
+  if constexpr (usable_iter<FMT, ITER>() == ITER) fused_nj<FMT, ITER>(a, st);
+  else fused_nj<FMT, 0>(a, st);
+}
+
 template <int FMT>
 static void fused_fmt(const FusedArgs &a, hipStream_t st) {
   switch (iter_of(FMT, a.H)) {
-  case 1: fused_nj<FMT, 1>(a, st); break;
-  case 2: fused_nj<FMT, 2>(a, st); break;
-  case 4: fused_nj<FMT, 4>(a, st); break;
+  case 1: fused_iter<FMT, 1>(a, st); break;
+  case 2: fused_iter<FMT, 2>(a, st); break;
+  case 4: fused_iter<FMT, 4>(a, st); break;
+  case 8: fused_iter<FMT, 8>(a, st); break;
   default: fused_nj<FMT, 0>(a, st); break;
   }
 }
 
 bool fused_supported(int fmt, int H, int E) {
-  size_t lds = 0;
-  int sr = 0;
-  switch (fmt) {
-  case kF32: lds = fused_lds_bytes<kF32>(H, E); sr = stage_rows<kF32>(H); break;
-  case kBF16: lds = fused_lds_bytes<kBF16>(H, E); sr = stage_rows<kBF16>(H); break;
-  case kINT8: lds = fused_lds_bytes<kINT8>(H, E); sr = stage_rows<kINT8>(H); break;
-  default: lds = fused_lds_bytes<kINT4>(H, E); sr = stage_rows<kINT4>(H); break;
-  }
-  const int epc = fmt == kF32 ? 4 : fmt == kBF16 ? 8 : fmt == kINT8 ? 16 : 32;
-  const int passes = fmt == kINT4 ? 1 : 2;
-  return sr > 0 && H / epc <= passes * kData && lds <= 160 * 1024 - 2048;  // static LDS < 1 KiB
+  (void)fmt;
+  return fused_lds_bytes(H, E) <= kLdsLimit;
 }
 
 __global__ void __launch_bounds__(256) zero_kernel(float *__restrict__ p, int64_t n) {

@@ -89,6 +89,7 @@ struct FusedArgs {
   int k_routed, with_shared;          // ranks of this launch
   int n_cu;                           // compute units of the device
   int nb, rb;                         // filled by the launcher: blocks per token, rows per block
+  int burst;                          // filled by the launcher: LDS holds the burst-mode down rows
 };
 hipError_t launch_expert_fused(const FusedArgs &a, hipStream_t st);
 bool fused_supported(int fmt, int H, int E);  // the LDS plan fits

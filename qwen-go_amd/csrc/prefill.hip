@@ -54,23 +54,6 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 __device__ __forceinline__ int swz_of(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_of(r)) << 4); }
 
-// LDS offset of a pointer into a __shared__ array.
-__device__ __forceinline__ uint32_t lds_offset(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
-// 16 bytes per lane from global memory straight into LDS at lds_wave_base +
-// 16 * lane (lds_wave_base is wave-uniform).  Issued through asm so that the
-// compiler does not track these loads: the GEMM waits for them explicitly
-// (wait_vm), and loads the compiler does track that were issued later only make
-// its own waits more conservative, never insufficient.
-__device__ __forceinline__ void dma16(const void *src, const unsigned char *lds_wave_base) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds_wave_base));
-  // one wait state between the M0 write and the LDS-direct load that reads it
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0)
-               : "memory", "m0");
-}
-
 // ------------------------------------------------------------------ prep
 
 __global__ void __launch_bounds__(256) prep_kernel(const float *__restrict__ x, int H,
@@ -202,7 +185,6 @@ __device__ __forceinline__ TileInfo tile_of(const PrefillPlan &p, int E, bool sh
 enum GemmKind { kGateUp = 0, kDown = 1 };
 
 constexpr int kWaves = kGemmThreads / 64;
-constexpr int kNStage = 3;
 constexpr int kAStage = kBM * kBK * 2;          // 32 KB
 constexpr int kBStage = 128 * kBK * 2;          // 16 KB
 constexpr int kStage = kAStage + kBStage;
