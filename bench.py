@@ -43,8 +43,12 @@ WORKLOADS = {
                 "qwen3-30b-a3b moe layer prefill T=2048, bf16 weights, router x4, skewed tokens, top-8 of 128"),
     "int8_decode": ("qwen3_30b_a3b_int8", 1, "E",
                     "qwen3-30b-a3b moe layer decode T=1, int8 group-32 experts, top-8 of 128"),
+    "int8_prefill": ("qwen3_30b_a3b_int8", 512, "E",
+                     "qwen3-30b-a3b moe layer prefill T=512, int8 group-32 experts, top-8 of 128"),
     "next_decode": ("qwen3_next", 1, "E",
                     "qwen3-next moe layer decode T=1, int4 group-32 experts + gated shared expert, top-10 of 512"),
+    "next_prefill": ("qwen3_next", 4096, "E",
+                     "qwen3-next moe layer prefill T=4096, int4 group-32 experts + gated shared expert, top-10 of 512"),
     "toy": ("toy", 16, "k", "toy moe layer T=16, f32, first-2 of 8 (reference selection)"),
 }
 
