@@ -103,11 +103,12 @@ struct PrefillPlan {
   float *wslot;                 // (slots) routing weight, or the shared gate
   int32_t *slot_of;             // (T, k) slot of each (token, rank)
   int32_t *grp_off, *grp_cnt;   // (E + 1) first slot and slot count per group
-  int32_t *tile_grp, *tile_m0;  // tile table: group and first row of each 128-slot tile
+  int32_t *tile_grp, *tile_m0;  // tile table: group and first row of each 256-slot tile
   int32_t *n_tiles;             // [0] routed tiles, [1] shared tiles (after the routed ones)
 };
 struct PrefillArgs {
   int T, H, E, k, I, Is, Imax;  // Imax = max(I, Is), the row pitch of act
+  int fmt;                      // expert (and shared expert) weight format: BF16, INT8 or INT4
   uint16_t *xb;                 // (T, H) x in bf16
   PrefillPlan p;
   const uint8_t *gu, *dn;       // gate_up (E, 2I, H); down transposed (E, I, H)

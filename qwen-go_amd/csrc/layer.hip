@@ -342,6 +342,7 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
     pa.I = I;
     pa.Is = Is;
     pa.Imax = std::max(I, Is);
+    pa.fmt = d.expert_fmt;
     pa.xb = l->xb;
     pa.p = l->plan;
     pa.gu = l->gu.w;

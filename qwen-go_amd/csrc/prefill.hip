@@ -9,9 +9,9 @@
 //             range, then a scatter of every pair into its expert's range
 //             (tok[slot], its routing weight, slot_of[t*k + r]).  The shared
 //             expert is group E, owning slots [T*k, T*k + T) in token order.
-//             Also the tile table: one entry per 128 slots of a group.
-//   gate_up   grouped GEMM: per (tile, 64 intermediate columns) a 128 x 128
-//             output block = 128 gathered bf16 rows of x times the expert's
+//             Also the tile table: one entry per 256 slots of a group.
+//   gate_up   grouped GEMM: per (tile, 64 intermediate columns) a 256 x 128
+//             output block = 256 gathered bf16 rows of x times the expert's
 //             gate rows [n0, n0+64) and up rows [I+n0, I+n0+64) over K = H,
 //             on v_mfma_f32_32x32x16_bf16 with f32 accumulation; SwiGLU in the
 //             epilogue (model/moe.go:64-75): act = silu(g) * u, stored bf16.
@@ -23,11 +23,12 @@
 // The slot order inside an expert comes from LDS atomics and may vary from run
 // to run; every output row depends only on its own token, so results do not.
 //
-// Tiles are staged through LDS with global_load_lds (16 bytes per lane) in
-// two stages, an XOR swizzle of the 16-byte chunks of each 128-byte row so
+// Expert weights are bf16, or int8 / int4 group-32 codes with fp16 scales
+// that the GEMMs dequantise to bf16 in LDS on the way to the MFMAs.  Tiles are
+// staged through LDS with global_load_lds (16 bytes per lane) in a ring of
+// three stages, an XOR swizzle of the 16-byte chunks of each 128-byte row so
 // that the MFMA operand reads (one row per lane) hit distinct banks.  The
-// down matrices are stored transposed, (I, H), for the decode kernel; their
-// tiles are transposed in registers on the way into LDS.
+// down matrices are stored transposed, (I, H), for the decode kernel.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -181,33 +182,117 @@ __device__ __forceinline__ TileInfo tile_of(const PrefillPlan &p, int E, bool sh
 //            (128 columns); a lane gathers its 8 K values of one column with
 //            8 two-byte LDS reads.  Chunks are XOR-ed with 4 in K rows 8..15
 //            of every 16 so that the two half-waves hit different banks.
+//
+// INT8 / INT4 group-32 experts (model/moe.go:124-157): the stage holds the B
+// codes (the same 64 K x 128 columns, 1 or 0.5 byte each) and their fp16
+// scales, loaded by global_load_lds like the rest.  Each wave then dequantises
+// the code pieces it loaded itself, w = code * scale (the f32 product of
+// quantLinear.dequantize) rounded to bf16, into a bf16 B tile laid out as
+// above (two such tiles alternate).  Since a wave converts only its own
+// loads, its own wait for them suffices and a K step keeps one barrier.
 
 enum GemmKind { kGateUp = 0, kDown = 1 };
 
 constexpr int kWaves = kGemmThreads / 64;
 constexpr int kAStage = kBM * kBK * 2;          // 32 KB
-constexpr int kBStage = 128 * kBK * 2;          // 16 KB
-constexpr int kStage = kAStage + kBStage;
+constexpr int kBStage = 128 * kBK * 2;          // 16 KB (bf16 B tile)
 constexpr int kADma = kAStage / 16 / kGemmThreads;  // 16-byte pieces per thread per stage
 constexpr int kBDma = kBStage / 16 / kGemmThreads;
 
-// s_waitcnt vmcnt(N) with the other counters untouched (gfx9 encoding).
+// LDS plan of a B format.
+template <int BF>
+struct BGeom {
+  static constexpr bool kQuant = BF == kINT8 || BF == kINT4;
+  static constexpr int kPieceElems = BF == kINT8 ? 16 : 32;         // elements per 16-byte code piece
+  static constexpr int kRaw = 128 * kBK * fmt_bytes_x2(BF) / 2;     // code bytes per stage
+  static constexpr int kBWaves = kQuant ? kRaw / 16 / 64 : kWaves;  // waves that load (and convert) B
+  static constexpr int kScale = kBWaves * 256;                      // fp16 scales per stage, 256 B per wave
+  static constexpr int kStage = kAStage + (kQuant ? kRaw + kScale : kBStage);
+  static constexpr int kTile = kQuant ? kBStage : 16;               // one dequantised B tile
+  static constexpr int kBLoads = kQuant ? 2 : kBDma;                // B loads per B-wave thread per step
+};
+
+// s_waitcnt vmcnt(N) with the other counters untouched (gfx9 encoding).  The
+// builtin is not a memory operation for the compiler, so the empty asm keeps
+// LDS reads of the landed data from being hoisted above it.
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+  asm volatile("" ::: "memory");
 }
+
+// Wait until this wave's LDS writes have completed.  s_barrier does not wait
+// for them on gfx950 (and the compiler inserts no wait before it), so data a
+// wave writes to LDS for the others needs this before the barrier.
+__device__ __forceinline__ void wait_lds_writes() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Workgroup barrier for the GEMM pipeline.  __syncthreads() also waits for
 // every outstanding global load (vmcnt(0)), which would drain the prefetched
 // stages.  Here each wave has already waited for its own LDS-direct loads of
-// the stage (wait_vm) and for its LDS reads of the previous stage (consumed by
-// its MFMAs), so the bare s_barrier suffices; the empty asm statements keep the
-// compiler from moving memory accesses across it.
+// the stage (wait_vm), for its LDS reads of the previous stage (consumed by its
+// MFMAs) and, where it wrote LDS, for those writes (wait_lds_writes), so the
+// bare s_barrier suffices; the empty asm statements keep the compiler from
+// moving memory accesses across it.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  const bf16x2_t h = __builtin_convertvector(v, bf16x2_t);
+  uint32_t r;
+  __builtin_memcpy(&r, &h, 4);
+  return r;
+}
+
+// Dequantised values of one 16-byte code piece, as packed bf16 pairs:
+// out[i] holds elements 2i and 2i+1.  scale(e) gives element e's scale.
+// INT8: 16 codes, value = code.  INT4: 32 elements, byte b holds element 2b in
+// its high nibble and 2b+1 in its low nibble, value = nibble - 8; the product
+// (nibble - 8) * s is formed as fma(nibble, s, -8 s), which rounds the same
+// exact value once.
+template <int BF, typename ScaleFn>
+__device__ __forceinline__ void dequant_piece(const uint4 v, ScaleFn scale,
+                                              uint32_t (&out)[BGeom<BF>::kPieceElems / 2]) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+  if constexpr (BF == kINT8) {
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int b = 0; b < 4; b += 2) {
+        const int e = 4 * q + b;
+        const float f0 = (float)(int8_t)((u[q] >> (8 * b)) & 0xffu) * scale(e);
+        const float f1 = (float)(int8_t)((u[q] >> (8 * b + 8)) & 0xffu) * scale(e + 1);
+        out[e / 2] = pack_bf16(f0, f1);
+      }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t hi = (u[q] >> 4) & 0x0f0f0f0fu, lo = u[q] & 0x0f0f0f0fu;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const int e = 8 * q + 2 * b;
+        const float s0 = scale(e), s1 = scale(e + 1);
+        const float f0 = fmaf((float)((hi >> (8 * b)) & 0xffu), s0, -8.0f * s0);
+        const float f1 = fmaf((float)((lo >> (8 * b)) & 0xffu), s1, -8.0f * s1);
+        out[e / 2] = pack_bf16(f0, f1);
+      }
+    }
+  }
+}
+
+// 4 bytes per lane from global memory into LDS at lds_wave_base + 4 * lane.
+__device__ __forceinline__ void dma4(const void *src, const unsigned char *lds_wave_base) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds_wave_base));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0)
+               : "memory", "m0");
 }
 
 // Work order, XCD-aware: workgroups are dealt to the 8 XCDs round-robin by
@@ -216,9 +301,11 @@ __device__ __forceinline__ void lds_barrier() {
 // the tile's A rows (gathered x, or act) for all of them.
 constexpr int kXcds = 8;
 
-template <int KIND>
-__global__ void __launch_bounds__(kGemmThreads) grouped_gemm_bf16(PrefillArgs a, int shared_launch, int ny) {
-  __shared__ __align__(16) unsigned char lds0[kStage], lds1[kStage], lds2[kStage];
+template <int KIND, int BF>
+__global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int shared_launch, int ny) {
+  using G = BGeom<BF>;
+  __shared__ __align__(16) unsigned char lds0[G::kStage], lds1[G::kStage], lds2[G::kStage];
+  __shared__ __align__(16) unsigned char btile[2][G::kTile];
   const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
   const int tile = (j / ny) * kXcds + xcd, chunk = j % ny;
   const TileInfo ti = tile_of(a.p, a.E, shared_launch, tile);
@@ -229,7 +316,9 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm_bf16(PrefillArgs a,
   const int K = KIND == kGateUp ? H : (sh ? a.Is : a.I);
   const int n0 = chunk * (KIND == kGateUp ? 64 : 128);
   if (n0 >= N) return;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, so branches on it are scalar
+  const int64_t rb = fmt_matrix_bytes(BF, 1, H);  // bytes of a gate/up row or of a transposed down row
 
   // A rows staged by this thread: row r = (i * kWaves + w) * 8 + lane / 8
   const uint16_t *arow[kADma];
@@ -242,31 +331,110 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm_bf16(PrefillArgs a,
     if constexpr (KIND == kGateUp) arow[i] = a.xb + (size_t)a.p.tok[ti.slot0 + m] * H;
     else arow[i] = a.act + (size_t)(ti.slot0 + m) * a.Imax;
   }
-  // B pieces staged by this thread
+  // B pieces staged by this thread (bf16), or its code piece and scale
+  // source (INT formats, waves below kBWaves)
   const uint16_t *bsrc[kBDma];
-#pragma unroll
-  for (int i = 0; i < kBDma; i++) {
-    const int sidx = (i * kWaves + w) * 64 + lane;  // 16-byte slot of the stage
-    if constexpr (KIND == kGateUp) {
-      const int r = sidx >> 3, c = (sidx & 7) ^ swz_of(r);
-      const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)ti.g * a.gu_bytes;
-      const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * H * 2;
-      const uint8_t *row = r < 64 ? gb + (size_t)(n0 + r) * H * 2 : ub + (size_t)(n0 + r - 64) * H * 2;
-      bsrc[i] = reinterpret_cast<const uint16_t *>(row) + c * 8;
-    } else {
-      const int kr = sidx >> 4, c = (sidx & 15) ^ (((kr >> 3) & 1) << 2);
-      const uint8_t *db = sh ? a.sdown : a.dn + (size_t)ti.g * a.dn_bytes;
-      bsrc[i] = reinterpret_cast<const uint16_t *>(db) + (size_t)kr * H + n0 + c * 8;
-    }
-  }
-  auto issue = [&](unsigned char *sa, int k0) {
-    unsigned char *sb = sa + kAStage;
-#pragma unroll
-    for (int i = 0; i < kADma; i++) dma16(arow[i] + k0 + achunk[i] * 8, sa + (i * kWaves + w) * 1024);
+  const uint8_t *qsrc = nullptr;   // code piece at K step 0
+  const uint16_t *ssrc = nullptr;  // scales at K step 0
+  const bool bwave = G::kBWaves == kWaves || w < G::kBWaves;
+  if constexpr (!G::kQuant) {
 #pragma unroll
     for (int i = 0; i < kBDma; i++) {
-      const uint16_t *src = KIND == kGateUp ? bsrc[i] + k0 : bsrc[i] + (size_t)k0 * H;
-      dma16(src, sb + (i * kWaves + w) * 1024);
+      const int sidx = (i * kWaves + w) * 64 + lane;  // 16-byte slot of the stage
+      if constexpr (KIND == kGateUp) {
+        const int r = sidx >> 3, c = (sidx & 7) ^ swz_of(r);
+        const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)ti.g * a.gu_bytes;
+        const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * rb;
+        const uint8_t *row = r < 64 ? gb + (size_t)(n0 + r) * rb : ub + (size_t)(n0 + r - 64) * rb;
+        bsrc[i] = reinterpret_cast<const uint16_t *>(row) + c * 8;
+      } else {
+        const int kr = sidx >> 4, c = (sidx & 15) ^ (((kr >> 3) & 1) << 2);
+        const uint8_t *db = sh ? a.sdown : a.dn + (size_t)ti.g * a.dn_bytes;
+        bsrc[i] = reinterpret_cast<const uint16_t *>(db) + (size_t)kr * H + n0 + c * 8;
+      }
+    }
+  } else if (bwave) {
+    const int gsc = H / kGroup;  // scales per gate/up row
+    if constexpr (KIND == kGateUp) {
+      // piece tid: row r, K elements [p * PE, +PE) of the stage
+      constexpr int PPR = kBK / G::kPieceElems;
+      const int r = tid / PPR, p = tid % PPR;
+      const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)ti.g * a.gu_bytes;
+      const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * rb;
+      const uint16_t *gs = sh ? a.sgate_s : a.gu_s + (size_t)ti.g * a.gu_scales;
+      const uint16_t *us = sh ? a.sup_s : gs + (size_t)a.I * gsc;
+      const int row = r < 64 ? n0 + r : n0 + r - 64;
+      qsrc = (r < 64 ? gb : ub) + (size_t)row * rb + p * 16;
+      ssrc = (r < 64 ? gs : us) + (size_t)row * gsc;  // + 2 kt: the row's two groups of the step
+    } else {
+      // piece tid: K row kr, columns [n0 + p * PE, +PE); lanes 0..15 load the
+      // wave's 128 column scales of its group
+      constexpr int PPR = 128 / G::kPieceElems;
+      const int kr = tid / PPR, p = tid % PPR;
+      const uint8_t *db = sh ? a.sdown : a.dn + (size_t)ti.g * a.dn_bytes;
+      const uint16_t *ds = sh ? a.sdown_s : a.dn_s + (size_t)ti.g * a.dn_scales;
+      qsrc = db + (size_t)kr * rb + (size_t)n0 * fmt_bytes_x2(BF) / 2 + p * 16;
+      ssrc = ds + n0 + (lane & 15) * 8;  // + ((k0 + first K row of the wave) / 32) * H
+    }
+  }
+  auto issue = [&](unsigned char *sa, int kt) {
+    const int k0 = kt * kBK;
+#pragma unroll
+    for (int i = 0; i < kADma; i++) dma16(arow[i] + k0 + achunk[i] * 8, sa + (i * kWaves + w) * 1024);
+    if constexpr (!G::kQuant) {
+      unsigned char *sb = sa + kAStage;
+#pragma unroll
+      for (int i = 0; i < kBDma; i++) {
+        const uint16_t *src = KIND == kGateUp ? bsrc[i] + k0 : bsrc[i] + (size_t)k0 * H;
+        dma16(src, sb + (i * kWaves + w) * 1024);
+      }
+    } else if (bwave) {
+      unsigned char *raw = sa + kAStage, *sc = raw + G::kRaw;
+      if constexpr (KIND == kGateUp) {
+        dma16(qsrc + (size_t)k0 * fmt_bytes_x2(BF) / 2, raw + w * 1024);
+        dma4(ssrc + 2 * kt, sc + w * 256);
+      } else {
+        dma16(qsrc + (size_t)k0 * rb, raw + w * 1024);
+        constexpr int RPW = 64 / G::kBWaves;  // K rows per wave
+        if (lane < 16) dma16(ssrc + (size_t)((k0 + w * RPW) / kGroup) * H, sc + w * 256);
+      }
+    }
+  };
+  // INT formats: dequantise this wave's code pieces of stage `cur` into `bt`
+  auto convert = [&](const unsigned char *cur, unsigned char *bt) {
+    if constexpr (G::kQuant) {
+      if (!bwave) return;
+      constexpr int PE = G::kPieceElems;
+      const unsigned char *raw = cur + kAStage, *sc = raw + G::kRaw + w * 256;
+      const uint4 v = *reinterpret_cast<const uint4 *>(raw + tid * 16);
+      uint32_t o[PE / 2];
+      if constexpr (KIND == kGateUp) {
+        constexpr int PPR = kBK / PE;
+        const int r = tid / PPR, p = tid % PPR;
+        const uint32_t sw = *reinterpret_cast<const uint32_t *>(sc + lane * 4);
+        const float s = f16_to_f32((uint16_t)(((p * PE) / kGroup) ? (sw >> 16) : (sw & 0xffffu)));
+        dequant_piece<BF>(v, [&](int) { return s; }, o);
+#pragma unroll
+        for (int c = 0; c < PE / 8; c++)
+          *reinterpret_cast<uint4 *>(bt + swz(r, p * (PE / 8) + c)) =
+              make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+      } else {
+        constexpr int PPR = 128 / PE;
+        const int kr = tid / PPR, p = tid % PPR;
+        uint4 sv[PE / 8];
+#pragma unroll
+        for (int c = 0; c < PE / 8; c++) sv[c] = *reinterpret_cast<const uint4 *>(sc + (p * PE + 8 * c) * 2);
+        dequant_piece<BF>(v, [&](int e) {
+          const uint32_t word = (&sv[e / 8].x)[(e % 8) / 2];
+          return f16_to_f32((uint16_t)((e & 1) ? (word >> 16) : (word & 0xffffu)));
+        }, o);
+        const int x = ((kr >> 3) & 1) << 2;
+#pragma unroll
+        for (int c = 0; c < PE / 8; c++)
+          *reinterpret_cast<uint4 *>(bt + kr * 256 + (((p * (PE / 8) + c) ^ x) << 4)) =
+              make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+      }
+      wait_lds_writes();  // the tile is read by every wave after the barrier
     }
   };
 
@@ -291,12 +459,16 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm_bf16(PrefillArgs a,
   // is the same at every step: past the end of K the batch re-reads the last K
   // slice into a stage that is never read again.
   auto step = [&](const unsigned char *cur, unsigned char *nxt2, int kt) {
-    wait_vm<kADma + kBDma>();  // stage kt landed; the batch of step kt + 1 may still fly
-    lds_barrier();             // stage kt visible to all; stage kt + 2 (read at kt - 1) is free
-    const unsigned char *sa = cur, *sb = cur + kAStage;
+    // stage kt landed; the batch of step kt + 1 may still fly
+    if (!G::kQuant || bwave) wait_vm<kADma + G::kBLoads>();
+    else wait_vm<kADma>();
+    unsigned char *bt = btile[kt & 1];
+    convert(cur, bt);
+    lds_barrier();  // stage kt visible to all; stage kt + 2 (read at kt - 1) is free
+    const unsigned char *sa = cur, *sb = G::kQuant ? bt : cur + kAStage;
     bf16x8_t av[2][4], bv[2][4];
     if (nb == 0) {  // nothing to multiply: keep the pipeline's loads in step
-      issue(nxt2, min(kt + 2, KT - 1) * kBK);
+      issue(nxt2, min(kt + 2, KT - 1));
       return;
     }
 #pragma unroll
@@ -323,7 +495,7 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm_bf16(PrefillArgs a,
         }
       }
     }
-    issue(nxt2, min(kt + 2, KT - 1) * kBK);
+    issue(nxt2, min(kt + 2, KT - 1));
 #pragma unroll
     for (int ks = 0; ks < 4; ks++)
 #pragma unroll
@@ -334,7 +506,7 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm_bf16(PrefillArgs a,
             acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b][ks], bv[q][ks], acc[b][q], 0, 0, 0);
   };
   issue(lds0, 0);
-  issue(lds1, min(1, KT - 1) * kBK);
+  issue(lds1, min(1, KT - 1));
   for (int kt = 0; kt < KT; kt += 3) {
     step(lds0, lds2, kt);
     if (kt + 1 < KT) step(lds1, lds0, kt + 1);
@@ -407,9 +579,9 @@ __global__ void __launch_bounds__(256) combine_kernel(const float *__restrict__ 
 // ------------------------------------------------------------- launchers
 
 bool prefill_supported(int expert_fmt, int shared_fmt, int H, int I, int Is) {
-  // bf16 experts; the shared expert (if any) in the same format
-  if (expert_fmt != kBF16) return false;
-  if (Is > 0 && shared_fmt != kBF16) return false;
+  // bf16, int8 or int4 experts; the shared expert (if any) in the same format
+  if (expert_fmt != kBF16 && expert_fmt != kINT8 && expert_fmt != kINT4) return false;
+  if (Is > 0 && shared_fmt != expert_fmt) return false;
   return H % 128 == 0 && I % 64 == 0 && (Is == 0 || Is % 64 == 0);
 }
 
@@ -432,7 +604,14 @@ template <int KIND>
 static hipError_t gemm_launch(const PrefillArgs &a, bool shared, int ny, hipStream_t st) {
   const int tiles = shared ? (a.T + kBM - 1) / kBM : prefill_max_tiles(a.T, a.k, a.E);
   const int blocks = (tiles + kXcds - 1) / kXcds * kXcds * ny;
-  QMOE_LAUNCH(grouped_gemm_bf16<KIND>, dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny);
+#define L(BF) QMOE_LAUNCH((grouped_gemm<KIND, BF>), dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny)
+  switch (a.fmt) {
+  case kBF16: L(kBF16); break;
+  case kINT8: L(kINT8); break;
+  case kINT4: L(kINT4); break;
+  default: return hipErrorInvalidValue;
+  }
+#undef L
   return hipGetLastError();
 }
 

@@ -272,18 +272,24 @@ def check_mfma_layer(cfg, hw, x, scope=None):
 
 
 PREFILL = [
-    # (router fmt, shared_inter, scope)
-    (qmoe.BF16, 0, 0),
-    (qmoe.BF16, 64, 16),
-    (qmoe.F32, 128, 0),
+    # (router fmt, expert and shared fmt, shared_inter, scope)
+    (qmoe.BF16, qmoe.BF16, 0, 0),
+    (qmoe.BF16, qmoe.BF16, 64, 16),
+    (qmoe.F32, qmoe.BF16, 128, 0),
+    (qmoe.BF16, qmoe.INT8G32, 0, 0),
+    (qmoe.BF16, qmoe.INT8G32, 64, 16),
+    (qmoe.F32, qmoe.INT4G32, 128, 0),
+    (qmoe.BF16, qmoe.INT4G32, 64, 16),
 ]
 
 
 @pytest.mark.parametrize("fmts", PREFILL, ids=lambda f: "-".join(map(str, f)))
 @pytest.mark.parametrize("T", [33, 100, 300])
 def test_prefill_layers(fmts, T):
-    rf, Is, scope = fmts
-    cfg = qmoe.LayerConfig(256, 16, 4, 128, Is, scope, rf, qmoe.BF16, qmoe.BF16, "prefill")
+    """Batched path for bf16, int8 and int4 experts (the INT formats are
+    dequantised to bf16 inside the GEMMs)."""
+    rf, ef, Is, scope = fmts
+    cfg = qmoe.LayerConfig(256, 16, 4, 128, Is, scope, rf, ef, ef, "prefill")
     announce(f"prefill layer fmts={fmts} T={T}")
     hw = qmoe.synthetic_weights(cfg, 300 + T, quantizer=oracle.host_quantizer)
     x = qmoe.synthetic_tokens(cfg, T, 300 + T)
@@ -322,6 +328,33 @@ def test_prefill_qwen3_shape_rows_are_independent():
         layer.close()
     assert np.array_equal(ids[:64], ids64)
     assert np.array_equal(out[:64].view(np.uint32), out64.view(np.uint32))
+    assert np.array_equal(idsp, ids[perm])
+    assert np.array_equal(outp.view(np.uint32), out[perm].view(np.uint32))
+    assert np.all(np.isfinite(out))
+
+
+@pytest.mark.parametrize("key,T_small,T_full", [("qwen3_30b_a3b_int8", 64, 512), ("qwen3_next", 48, 4096)])
+def test_prefill_quantized_shapes(key, T_small, T_full):
+    """Qwen3-30B-A3B int8 experts (T=512) and the Qwen3-Next int4 layer with its
+    int4 shared expert (T=4096): T_small tokens against the oracle, then the
+    full batch, whose first T_small rows must equal the small batch's bit for
+    bit, and a permuted full batch, whose rows must follow the permutation."""
+    cfg = qmoe.CONFIGS[key]
+    cfg = cfg.with_(select_scope=cfg.n_experts)
+    announce(f"prefill {key} T={T_small} vs oracle, T={T_full} row independence")
+    hw = qmoe.synthetic_weights(cfg, T_full, quantizer=qmoe.device_quantizer)
+    x = qmoe.synthetic_tokens(cfg, T_full, T_full)
+    out_s, ids_s, _ = check_mfma_layer(cfg, hw, x[:T_small])
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(x)
+        perm = np.random.default_rng(2).permutation(T_full)
+        outp, idsp, _ = layer.forward(np.ascontiguousarray(x[perm]))
+    finally:
+        layer.close()
+    assert np.array_equal(ids[:T_small], ids_s)
+    assert np.array_equal(out[:T_small].view(np.uint32), out_s.view(np.uint32))
     assert np.array_equal(idsp, ids[perm])
     assert np.array_equal(outp.view(np.uint32), out[perm].view(np.uint32))
     assert np.all(np.isfinite(out))
