@@ -286,13 +286,21 @@ def main():
         tot_n += n
     stage_avg_us = {qmoe.STAGE_NAMES[s]: round(1e3 * tot_ms[s] / max(tot_n[s], 1), 3)
                     for s in all_stages if tot_n[s]}
+    if tot_n[qmoe.STAGE_FUSED] and not tot_n[qmoe.STAGE_ROUTER]:
+        # T = 1: the expert kernel computes the router partials itself and reads the router
+        for b in per_x_bytes:
+            b[qmoe.STAGE_FUSED] += b[qmoe.STAGE_ROUTER] - T * cfg.n_experts * 4
+            b[qmoe.STAGE_ROUTER] = 0
     # dominant HBM-bound kernel: the one with the most time among the weight-streaming stages
     weight_stages = [qmoe.STAGE_GATE_UP, qmoe.STAGE_DOWN, qmoe.STAGE_FUSED]
     dom = max(weight_stages, key=lambda s: tot_ms[s])
 
-    # timed region: only the dominant kernel carries events
-    for L in layers:
-        L.profile_enable([dom])
+    # timed region: only the dominant kernel carries events, and only on the
+    # first weight copy (every `copies`-th step) -- a launch with events costs
+    # the host about 20 us more, which would otherwise make a decode step
+    # host-bound
+    for i, L in enumerate(layers):
+        L.profile_enable([dom] if i == 0 else [])
         L.profile_read(reset=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -307,7 +315,7 @@ def main():
         dom_ms += ms[dom]
         dom_n += int(n[dom])
     dom_avg_s = dom_ms / 1e3 / max(dom_n, 1)
-    dom_bytes = float(np.mean([per_x_bytes[s % n_x][dom] for s in range(args.steps)]))
+    dom_bytes = float(np.mean([per_x_bytes[s % n_x][dom] for s in range(0, args.steps, copies)]))
     achieved = dom_bytes / dom_avg_s / 1e9
     mfma_path = layers[0].forward_path(T) == qmoe.PATH_MFMA
     dom_flops = stage_flops(cfg, T).get(dom, 0) if mfma_path else 0

@@ -26,6 +26,7 @@
 // entry.  The atomics make the order of the final f32 sums run-dependent
 // (within f32 rounding of the reference's rank-ordered sum).
 #include "gemv_common.hpp"
+#include "router_common.hpp"
 #include "select.hpp"
 
 namespace qmoe {
@@ -42,6 +43,40 @@ __host__ __device__ inline size_t fused_head_bytes(int H, int E) {
   return ((size_t)(3 * H + E) * 4 + 15) / 16 * 16;
 }
 constexpr size_t kLdsLimit = 160 * 1024 - 2048;  // static LDS < 1 KiB
+
+// Longest wait for the other workgroups' router partials, in s_memrealtime
+// ticks (100 MHz): 2 ms.  They normally arrive within a few microseconds; a
+// device that does not run every workgroup of the launch at once would
+// otherwise leave the waiting workgroups spinning.
+constexpr uint64_t kExchangeTicks = 200000;
+
+// Polls the 2E tagged router words of this call until every one carries `tag`
+// (or the wait times out: false).  Lane l receives expert l + 64 j in S[j],
+// B[j] (S = -inf, B = 0 past E).
+template <int NJ>
+__device__ __forceinline__ bool poll_router_words(const uint64_t *rtag, int E, uint32_t tag, double (&S)[NJ],
+                                                  double (&B)[NJ]) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (;;) {
+    bool mine = true;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const int e = lane + 64 * j;
+      S[j] = -INFINITY;
+      B[j] = 0.0;
+      if (e < E) {
+        const uint64_t ws = __hip_atomic_load(rtag + 2 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t wb = __hip_atomic_load(rtag + 2 * e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        mine = mine && (ws & 0xffu) == tag && (wb & 0xffu) == tag;
+        S[j] = untag_word(ws);
+        B[j] = untag_word(wb);
+      }
+    }
+    if (__all(mine)) return true;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > kExchangeTicks) return false;
+  }
+}
 __host__ inline size_t fused_burst_bytes() { return (size_t)(kData / 64) * kBurstKB * 1024; }
 __host__ inline bool fused_burst_fits(int H, int E) { return fused_head_bytes(H, E) + fused_burst_bytes() <= kLdsLimit; }
 __host__ inline size_t fused_lds_bytes(int H, int E) {
@@ -116,6 +151,33 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   float *lt = red + 2 * H;    // exact logits (fallback)
   unsigned char *burst_lds = smem + fused_head_bytes(H, a.E);
 
+  // ---- router partials computed in-kernel (T = 1): waves 1..7 of the
+  // workgroups take one expert each (expert e: workgroup e % G, wave
+  // 1 + e / G), publish {S, B} as tagged words, and zero their slice of out
+  // first -- the release fence orders those zeros before the words, which
+  // every workgroup reads (with an acquire) before its atomics into out.
+  if (a.fused_router && threadIdx.x >= kCtl) {
+    const int G = gridDim.x;
+    const int e = blockIdx.x + ((threadIdx.x >> 6) - 1) * G;
+    if (e < a.E) {
+      const int lane = threadIdx.x & 63;
+      const uint8_t *row = a.rw + (size_t)e * fmt_matrix_bytes(kBF16, 1, H);
+      double S, B;
+      if (a.fused_router == 1) router_sb_wave<kBF16, 1>(a.x, H, row, nullptr, S, B);
+      else if (a.fused_router == 2) router_sb_wave<kBF16, 2>(a.x, H, row, nullptr, S, B);
+      else router_sb_wave<kBF16, 4>(a.x, H, row, nullptr, S, B);
+      const int Z = (H + a.E - 1) / a.E;
+      for (int j = e * Z + lane; j < min(H, e * Z + Z); j += 64) a.out[j] = 0.0f;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      if (lane == 0) {
+        uint64_t ws, wb;
+        tagged_sb(S, B, a.epoch, ws, wb);
+        __hip_atomic_store(a.rtag + 2 * e, ws, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.rtag + 2 * e + 1, wb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+
   // ---- block -> (token, rows [u0, u1) of the token's flattened rows)
   const int t = blockIdx.x / a.nb;
   if (t >= a.T) return;
@@ -149,7 +211,7 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   auto run_rank = [&](int q) { return q ? rank1 : rank0; };
   const bool ctl = threadIdx.x < kCtl;
   const int dt = threadIdx.x;  // row-streaming thread index (all threads)
-  const bool writer = blockIdx.x % a.nb == 0 && a.sb && a.k_routed > 0;
+  const bool writer = blockIdx.x % a.nb == 0 && (a.sb || a.fused_router) && a.k_routed > 0;
 
   if (threadIdx.x < 64) s_spec[threadIdx.x] = 0;
   if (threadIdx.x == 0) s_xready = 0;
@@ -479,7 +541,27 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   if (ctl) {
     // ---- control wave: routing; the shared gate for a shared run
     const bool has_routed = rank0 != a.k;
-    if (has_routed && a.sb) {
+    if (a.fused_router) {
+      // every workgroup waits for the words, also one with only shared-expert
+      // rows: seeing them orders out's zeros before its atomics
+      double S[NJ], B[NJ];
+      if (poll_router_words<NJ>(a.rtag, a.E, a.epoch, S, B)) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // out's zeros are visible from here on
+        if (has_routed) {
+          const bool ok = certified_select_regs<NJ>(S, B, a.E, a.k, a.scope, writer ? a.ids : nullptr,
+                                                    writer ? a.weights : nullptr, s_ids, s_w, -2, s_spec);
+          need_exact = !ok;
+        }
+      } else {
+        // timed out: flag it for the host (the call's result is not
+        // trustworthy), stream expert 0 tentatively and route this workgroup
+        // with the exact logits so that every wave still finishes
+        if (threadIdx.x == 0) __hip_atomic_store(a.xchg_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (has_routed && threadIdx.x < a.k)
+          __hip_atomic_store(&s_spec[threadIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        need_exact = has_routed;
+      }
+    } else if (has_routed && a.sb) {
       const bool ok = certified_select_nj<NJ>(a.sb + (size_t)t * a.E * 2, a.E, a.k, a.scope,
                                               writer ? a.ids + (size_t)t * a.k : nullptr,
                                               writer ? a.weights + (size_t)t * a.k : nullptr, s_ids, s_w, -2,

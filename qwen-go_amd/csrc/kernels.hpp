@@ -90,6 +90,15 @@ struct FusedArgs {
   int n_cu;                           // compute units of the device
   int nb, rb;                         // filled by the launcher: blocks per token, rows per block
   int burst;                          // filled by the launcher: LDS holds the burst-mode down rows
+  // T = 1, bf16 router: the kernel computes the router partials itself
+  // (fused_router = router chunks per lane, 1, 2 or 4; sb null), exchanges
+  // them between its workgroups through rtag (2 words per expert) tagged with
+  // epoch (1..255, a new value every call) and zeroes out itself.  xchg_err
+  // (host-visible) is set if the exchange times out.
+  int fused_router;
+  uint64_t *rtag;
+  uint32_t epoch;
+  int *xchg_err;
 };
 hipError_t launch_expert_fused(const FusedArgs &a, hipStream_t st);
 bool fused_supported(int fmt, int H, int E);  // the LDS plan fits

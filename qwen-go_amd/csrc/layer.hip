@@ -65,6 +65,12 @@ struct qmoe_layer {
   float *sg = nullptr, *y = nullptr;
   PrefillPlan plan{};
   unsigned int *fallbacks = nullptr;  // tokens routed by the exact fallback
+  // decode (T = 1): the expert kernel computes the router partials itself and
+  // exchanges them between its workgroups as tagged words (2 per expert)
+  uint64_t *rtag = nullptr;
+  uint32_t rtag_epoch = 0;            // tag of the last call, 1..255
+  int *xchg_err_host = nullptr;       // host-visible flag: an exchange timed out
+  int *xchg_err_dev = nullptr;
 
   // optional per-stage event timing (qmoe_profile_*)
   uint32_t prof_mask = 0;
@@ -149,6 +155,8 @@ void free_all(qmoe_layer *l) {
   l->ws_T = 0;
   if (l->stream) (void)hipStreamDestroy(l->stream);
   l->stream = nullptr;
+  if (l->xchg_err_host) (void)hipHostFree(l->xchg_err_host);
+  l->xchg_err_host = l->xchg_err_dev = nullptr;
 }
 
 // Moves n stored matrices in the reference layout from device staging into
@@ -374,8 +382,18 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
     return QMOE_OK;
   }
 
-  const bool cert = T <= kMaxGemvTokens && router_certified_supported(l->router);
-  if (cert) {
+  // T = 1 with a bf16 router of at most 4 chunks per lane: the expert kernel
+  // computes the router partials itself (no router launch) and zeroes out.
+  const int rcpl = (H / 8 + 63) / 64;
+  const bool fused_router = T == 1 && l->router.fmt == kBF16 && H % 8 == 0 && (rcpl == 1 || rcpl == 2 || rcpl == 4) &&
+                            E <= 7 * l->n_cu && fused_supported(l->gu.fmt, H, E);
+  if (fused_router && *l->xchg_err_host)
+    return fail(l, QMOE_ERR_HIP, "an earlier decode call timed out exchanging router partials between workgroups "
+                                 "(the device did not run all of its workgroups at once)");
+  const bool cert = !fused_router && T <= kMaxGemvTokens && router_certified_supported(l->router);
+  if (fused_router) {
+    // nothing to launch before the expert kernel
+  } else if (cert) {
     STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, d_out, st), "router launch");
   } else {
     STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
@@ -417,6 +435,13 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   f.ids = ids;
   f.weights = wts;
   f.fallbacks = l->fallbacks;
+  if (fused_router) {
+    l->rtag_epoch = l->rtag_epoch % 255 + 1;
+    f.fused_router = rcpl;
+    f.rtag = l->rtag;
+    f.epoch = l->rtag_epoch;
+    f.xchg_err = l->xchg_err_dev;
+  }
   f.out = d_out;
   f.k_routed = k;
   f.with_shared = Is > 0 && d.shared_fmt == d.expert_fmt;
@@ -427,6 +452,7 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
     f.fmt = d.shared_fmt;
     f.k_routed = 0;
     f.with_shared = 1;
+    f.fused_router = 0;
     STAGE(l, QMOE_STAGE_FUSED, st, launch_expert_fused(f, st), "fused shared-expert launch");
   }
   return QMOE_OK;
@@ -517,6 +543,30 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
     }
     l->owned.push_back(b);
     l->fallbacks = (unsigned int *)b.p;
+  }
+  {
+    DevBuf b;
+    b.n = (size_t)E * 16;
+    if (hipMalloc(&b.p, b.n) != hipSuccess || hipMemset(b.p, 0, b.n) != hipSuccess) {
+      (void)hipGetLastError();
+      free_all(l);
+      delete l;
+      return fail(nullptr, QMOE_ERR_NOMEM, "hipMalloc of the router exchange words failed");
+    }
+    l->owned.push_back(b);
+    l->rtag = (uint64_t *)b.p;
+    void *hp = nullptr, *dp = nullptr;
+    if (hipHostMalloc(&hp, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+        hipHostGetDevicePointer(&dp, hp, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      if (hp) (void)hipHostFree(hp);
+      free_all(l);
+      delete l;
+      return fail(nullptr, QMOE_ERR_NOMEM, "hipHostMalloc of the exchange flag failed");
+    }
+    l->xchg_err_host = (int *)hp;
+    l->xchg_err_dev = (int *)dp;
+    *l->xchg_err_host = 0;
   }
   if (Is > 0) {
     DevBuf b;

@@ -10,6 +10,7 @@
 // separately rounded, as Go on amd64 does.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "router_common.hpp"
 #include "select.hpp"
 
 #include <math.h>
@@ -17,21 +18,6 @@
 namespace qmoe {
 
 constexpr int kMaxE = 1024;
-
-// Widens element k of a stored router row to f32 exactly as the reference:
-// bf16 -> bits << 16, int8 -> float(code) * scale, int4 -> float(nibble-8) * scale.
-template <int FMT>
-__device__ __forceinline__ void router_chunk(const uint8_t *__restrict__ row,
-                                             const uint16_t *__restrict__ srow, int chunk,
-                                             float (&w)[Chunk<FMT>::kElems]) {
-#pragma clang fp contract(off)
-  float sc;
-  load_chunk<FMT>(row, srow, chunk, w, sc);
-  if constexpr (fmt_quant(FMT)) {
-#pragma unroll
-    for (int i = 0; i < Chunk<FMT>::kElems; i++) w[i] = w[i] * sc;
-  }
-}
 
 // One thread per (token, expert); used when T is small.  The token's x row is
 // staged in LDS and read as a broadcast; each lane streams its own router row.
@@ -222,25 +208,13 @@ hipError_t launch_softmax_select(const float *logits, int T, int E, int k, int s
 }
 
 // ---------------------------------------------------------------------------
-// Certified router for decode-sized T.
-//
-// The exact logits above cost one dependent f32 add per h per (token, expert)
-// -- about 2 instructions x H cycles of latency, several microseconds at
-// T = 1.  This path computes the same products p_h = fl(x_h * w_h) (identical
-// IEEE multiplies) and sums them in f64 across the wavefront, giving S ~ the
-// exact sum.  The reference's sequential f32 sum s_H differs from S by at most
-//   B = u (1 + 2 H u) sum_h |S_h|,   u = 2^-24, S_h the exact prefix sums
-// (each add rounds with relative error <= u; the f64 prefix sums come from a
-// wavefront scan).  Selection (select.hpp, certified_select_lds) then runs on
-// S and certifies every rank; a token that fails (a near tie, or an exact tie
-// that the index must break) is recomputed with the exact sequential logits.
-// Either way the ids are the reference's bit for bit.
+// Certified router for decode-sized T (router_common.hpp): the exact logits
+// above cost one dependent f32 add per h per (token, expert) -- about
+// 2 instructions x H cycles of latency, several microseconds at T = 1.  This
+// path writes {S, B} per (token, expert) instead; selection (select.hpp)
+// certifies every rank on them or recomputes the token's exact logits, so the
+// ids are the reference's bit for bit either way.
 // ---------------------------------------------------------------------------
-
-__device__ __forceinline__ double seq_sum_bound(double babs, double pabs, int H) {
-  const double u = 0x1p-24;
-  return u * (1.0 + 2.0 * H * u + 1e-9) * babs + 1e-12 * pabs;
-}
 
 // One wavefront per (token, expert) writes sb[(t, e)] = {S, B}.  Block (0, t)
 // also zeroes out[t] when zero_out != nullptr (the fused expert kernel
@@ -250,59 +224,20 @@ __global__ void __launch_bounds__(256) router_sb_kernel(const float *__restrict_
                                                         const uint8_t *__restrict__ w,
                                                         const uint16_t *__restrict__ s, int E,
                                                         double *__restrict__ sb, float *__restrict__ zero_out) {
-#pragma clang fp contract(off)
-  constexpr int EPC = Chunk<FMT>::kElems;
-  constexpr int NP = CPL * EPC;  // products per lane
   const int t = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int e = blockIdx.x * 4 + wave;
-  const int nch = H / EPC;
-  const float *xt = x + (size_t)t * H;
   if (zero_out && blockIdx.x == 0)
     for (int i = threadIdx.x; i < H; i += 256) zero_out[(size_t)t * H + i] = 0.0f;
   if (e >= E) return;
   const uint8_t *row = w + (size_t)e * fmt_matrix_bytes(FMT, 1, H);
   const uint16_t *srow = fmt_quant(FMT) ? s + (size_t)e * (H / kGroup) : nullptr;
-  float p[NP];
-#pragma unroll
-  for (int c = 0; c < CPL; c++) {
-    const int ch = lane * CPL + c;
-    float wv[EPC];
-    if (ch < nch) {
-      router_chunk<FMT>(row, srow, ch, wv);
-#pragma unroll
-      for (int i = 0; i < EPC; i += 4) {
-        const float4 xv = *reinterpret_cast<const float4 *>(xt + ch * EPC + i);
-        p[c * EPC + i + 0] = xv.x * wv[i + 0];
-        p[c * EPC + i + 1] = xv.y * wv[i + 1];
-        p[c * EPC + i + 2] = xv.z * wv[i + 2];
-        p[c * EPC + i + 3] = xv.w * wv[i + 3];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < EPC; i++) p[c * EPC + i] = 0.0f;
-    }
-  }
-  double tot = 0.0, pabs = 0.0;
-#pragma unroll
-  for (int i = 0; i < NP; i++) {
-    tot += (double)p[i];
-    pabs += fabs((double)p[i]);
-  }
-  const double inc = wave_incl_scan_f64(tot);  // lane totals -> exact prefix sums
-  double run = inc - tot, babs = 0.0;
-#pragma unroll
-  for (int i = 0; i < NP; i++) {
-    run += (double)p[i];
-    babs += fabs(run);
-  }
-  const double S = readlane_f64(inc, 63);
-  babs = wave_sum_f64(babs);
-  pabs = wave_sum_f64(pabs);
+  double S, B;
+  router_sb_wave<FMT, CPL>(x + (size_t)t * H, H, row, srow, S, B);
   if (lane == 0) {
     double *d = sb + ((size_t)t * E + e) * 2;
     d[0] = S;
-    d[1] = seq_sum_bound(babs, pabs, H);
+    d[1] = B;
   }
 }
 

@@ -218,27 +218,20 @@ __device__ __forceinline__ double wave_max_f64(double v) { return dkey_inv(wave_
 // Weights come from the f64 softmax of S.  When spec_slot is given, the
 // tentative expert of rank spec_rank is published there (as id + 1) as soon
 // as its round ends, before certification.
+// certified_select_regs takes the pairs already in registers: lane l holds
+// expert l + 64 j in S[j], B[j] (S = -inf, B = 0 past E).
 template <int NJ>
-__device__ __forceinline__ bool certified_select_nj(const double *__restrict__ sb, int E, int k, int scope,
-                                                    int32_t *g_ids, float *g_w, int *s_ids, float *s_w,
-                                                    int spec_rank = -1, int *spec_slot = nullptr) {
+__device__ __forceinline__ bool certified_select_regs(const double (&S)[NJ], const double (&B)[NJ], int E, int k,
+                                                      int scope, int32_t *g_ids, float *g_w, int *s_ids,
+                                                      float *s_w, int spec_rank = -1, int *spec_slot = nullptr) {
   // spec_rank == -2: publish every rank's tentative expert to spec_slot[rank]
   const int lane = threadIdx.x & 63;
-  double S[NJ], B[NJ];
   float key[NJ];
   float mh = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
     const int e = lane + 64 * j;
-    if (e < E) {
-      const double2 v = reinterpret_cast<const double2 *>(sb)[e];
-      S[j] = v.x;
-      B[j] = v.y;
-      mh = fmaxf(mh, (float)(S[j] + B[j]));
-    } else {
-      S[j] = -INFINITY;
-      B[j] = 0.0;
-    }
+    if (e < E) mh = fmaxf(mh, (float)(S[j] + B[j]));
     key[j] = e < scope ? (float)S[j] : -INFINITY;
   }
   // upper bound of the reference's max logit (f32 rounding covered by 2^-20)
@@ -337,6 +330,27 @@ __device__ __forceinline__ bool certified_select_nj(const double *__restrict__ s
     }
   }
   return true;
+}
+
+template <int NJ>
+__device__ __forceinline__ bool certified_select_nj(const double *__restrict__ sb, int E, int k, int scope,
+                                                    int32_t *g_ids, float *g_w, int *s_ids, float *s_w,
+                                                    int spec_rank = -1, int *spec_slot = nullptr) {
+  const int lane = threadIdx.x & 63;
+  double S[NJ], B[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      const double2 v = reinterpret_cast<const double2 *>(sb)[e];
+      S[j] = v.x;
+      B[j] = v.y;
+    } else {
+      S[j] = -INFINITY;
+      B[j] = 0.0;
+    }
+  }
+  return certified_select_regs<NJ>(S, B, E, k, scope, g_ids, g_w, s_ids, s_w, spec_rank, spec_slot);
 }
 
 // Dispatch on the number of expert slots per lane.

@@ -192,6 +192,43 @@ def test_qwen3_next_int4_decode():
     check_layer(cfg, hw, x)
 
 
+def test_qwen3_next_int4_decode_T1():
+    """T = 1: the expert kernel computes the router partials itself; 512
+    experts put two router rows on some workgroups."""
+    cfg = qmoe.CONFIGS["qwen3_next"].with_(select_scope=512)
+    announce("qwen3-next int4g32 + shared T=1 scope=E, in-kernel router")
+    hw = qmoe.synthetic_weights(cfg, 98, quantizer=qmoe.device_quantizer)
+    x = qmoe.synthetic_tokens(cfg, 1, 98)
+    check_layer(cfg, hw, x)
+
+
+@pytest.mark.parametrize("fmts", [(qmoe.BF16, 512, 0), (qmoe.INT8G32, 1024, 64)], ids=["bf16-H512", "int8-H1024-shared"])
+def test_decode_router_exchange_many_calls(fmts):
+    """600 T = 1 calls on one handle: the tag of the exchanged router words
+    wraps around (1..255) twice; every call's ids must equal the oracle's and
+    its output stay within the decode bar."""
+    ef, H, Is = fmts
+    cfg = qmoe.LayerConfig(H, 16, 4, 128, Is, 16, qmoe.BF16, ef, ef, "exchange")
+    announce(f"decode router exchange, 600 calls, fmts={fmts}")
+    hw = qmoe.synthetic_weights(cfg, 600 + H, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, 600, 600 + H)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        outs, idss = [], []
+        for i in range(600):
+            o, ids, _ = layer.forward(x[i:i + 1])
+            outs.append(o)
+            idss.append(ids)
+    finally:
+        layer.close()
+    ref, rids, _ = oracle.OracleLayer(hw, scope=16).forward(x)
+    ids = np.concatenate(idss)
+    assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
+    err = rel_err(np.concatenate(outs), ref)
+    assert err <= TOL_F32, f"normwise relative error {err:.3e} > {TOL_F32}"
+
+
 @pytest.mark.parametrize("T", [1, 5, 40])
 def test_router_exact_ties(T):
     """Identical router rows give exactly equal logits; the reference breaks the
