@@ -56,6 +56,20 @@ __device__ __forceinline__ void dma16(const void *src, const unsigned char *lds_
                : "memory", "m0");
 }
 
+// The same with the nontemporal hint (streamed weights that are read once).
+__device__ __forceinline__ void dma16_nt(const void *src, const unsigned char *lds_wave_base) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds_wave_base));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0)
+               : "memory", "m0");
+}
+
+// 16-byte load with the nontemporal hint.
+__device__ __forceinline__ uint4 load_nt(const void *p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64);
 // every lane of the group receives the sum.
 __device__ __forceinline__ float group_sum(float v, int width) {

@@ -50,6 +50,20 @@ constexpr size_t kLdsLimit = 160 * 1024 - 2048;  // static LDS < 1 KiB
 // otherwise leave the waiting workgroups spinning.
 constexpr uint64_t kExchangeTicks = 200000;
 
+// Waits until the n tagged words (one per workgroup, saying that its slice of
+// out is zero) carry `tag` (false: timed out).
+__device__ __forceinline__ bool poll_zero_flags(const uint32_t *ztag, int n, uint32_t tag) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (;;) {
+    bool mine = true;
+    for (int i = lane; i < n; i += 64)
+      mine = mine && __hip_atomic_load(ztag + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
+    if (__all(mine)) return true;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > kExchangeTicks) return false;
+  }
+}
+
 // Polls the 2E tagged router words of this call until every one carries `tag`
 // (or the wait times out: false).  Lane l receives expert l + 64 j in S[j],
 // B[j] (S = -inf, B = 0 past E).
@@ -153,28 +167,38 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
 
   // ---- router partials computed in-kernel (T = 1): waves 1..7 of the
   // workgroups take one expert each (expert e: workgroup e % G, wave
-  // 1 + e / G), publish {S, B} as tagged words, and zero their slice of out
-  // first -- the release fence orders those zeros before the words, which
-  // every workgroup reads (with an acquire) before its atomics into out.
+  // 1 + e / G) and publish {S, B} as tagged words, which carry their own
+  // validity.  Wave 7 of every workgroup zeroes its slice of out and then
+  // (release) tags a per-workgroup word; every workgroup waits for all of
+  // those (acquire) before its atomics into out -- off the critical path,
+  // since that is long after the start.
   if (a.fused_router && threadIdx.x >= kCtl) {
     const int G = gridDim.x;
-    const int e = blockIdx.x + ((threadIdx.x >> 6) - 1) * G;
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int e = blockIdx.x + (wv - 1) * G;
     if (e < a.E) {
-      const int lane = threadIdx.x & 63;
       const uint8_t *row = a.rw + (size_t)e * fmt_matrix_bytes(kBF16, 1, H);
       double S, B;
       if (a.fused_router == 1) router_sb_wave<kBF16, 1>(a.x, H, row, nullptr, S, B);
       else if (a.fused_router == 2) router_sb_wave<kBF16, 2>(a.x, H, row, nullptr, S, B);
       else router_sb_wave<kBF16, 4>(a.x, H, row, nullptr, S, B);
-      const int Z = (H + a.E - 1) / a.E;
-      for (int j = e * Z + lane; j < min(H, e * Z + Z); j += 64) a.out[j] = 0.0f;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       if (lane == 0) {
         uint64_t ws, wb;
         tagged_sb(S, B, a.epoch, ws, wb);
         __hip_atomic_store(a.rtag + 2 * e, ws, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(a.rtag + 2 * e + 1, wb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+    }
+    if (wv == kFusedBlock / 64 - 1) {
+      // The zeros are agent-scope stores, which write through the L2; once
+      // this wave's stores have completed (vmcnt(0)) they are visible device
+      // wide, so the flag needs no L2 writeback (a release fence here would
+      // write back the whole L2 and stall the router rows' loads).
+      const int Z = (H + G - 1) / G;
+      for (int j = blockIdx.x * Z + lane; j < min(H, (int)blockIdx.x * Z + Z); j += 64)
+        __hip_atomic_store(a.out + j, 0.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (lane == 0) __hip_atomic_store(a.ztag + blockIdx.x, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
@@ -239,13 +263,17 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   // touches consecutive words (no LDS bank conflicts).
   auto pos = [&](int ch, int e) { return e * nch + ch; };
   const int lpr = lanes_per_row(nch);
-  const int groups = kData / lpr;
-  const int g = dt / lpr, sl = dt % lpr;
-  const int rs = (int)((int64_t)g * nrows / groups), re = (int)((int64_t)(g + 1) * nrows / groups);
-  // burst mode (block-uniform): every lane group is one wave with at most
-  // burst_rows rows, and the LDS holds the burst regions
-  const bool use_burst = a.burst && lpr == 64 && (nrows + groups - 1) / groups <= burst_rows<FMT, ITER>() &&
+  // burst mode (block-uniform): the lane groups are waves 1..7 -- the control
+  // wave, busy with the selection until late, takes no rows -- each with at
+  // most burst_rows rows, and the LDS holds the burst regions
+  constexpr int kBurstGroups = kData / 64 - 1;
+  const bool use_burst = a.burst && lpr == 64 &&
+                         (nrows + kBurstGroups - 1) / kBurstGroups <= burst_rows<FMT, ITER>() &&
                          2 * H * 4 <= kBurstKB * 1024;
+  const int groups = use_burst ? kBurstGroups : kData / lpr;
+  const int g = use_burst ? dt / 64 - 1 : dt / lpr, sl = dt % lpr;  // g = -1: no rows
+  const int rs = g < 0 ? 0 : (int)((int64_t)g * nrows / groups);
+  const int re = g < 0 ? 0 : (int)((int64_t)(g + 1) * nrows / groups);
 
   // expert of run q: tentative (published in s_spec, for the data waves) or
   // final (s_ids); both live in LDS in either routing mode
@@ -347,7 +375,7 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
           if (r < n) {
 #pragma unroll
             for (int c = 0; c < IT; c++)
-              dma16(bp[r].d + (size_t)(sl + c * lpr) * 16, wl + (r * IT + c) * 1024);
+              dma16_nt(bp[r].d + (size_t)(sl + c * lpr) * 16, wl + (r * IT + c) * 1024);
           }
         }
 #pragma unroll
@@ -356,8 +384,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
 #pragma unroll
             for (int c = 0; c < IT; c++) {
               const size_t off = (size_t)(sl + c * lpr) * 16;
-              bg[r][c] = *reinterpret_cast<const uint4 *>(bp[r].g + off);
-              bu[r][c] = *reinterpret_cast<const uint4 *>(bp[r].u + off);
+              bg[r][c] = load_nt(bp[r].g + off);
+              bu[r][c] = load_nt(bp[r].u + off);
             }
             if constexpr (fmt_quant(FMT)) {
               // the lane's outputs: chunk c covers EPC consecutive outputs
@@ -542,24 +570,21 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
     // ---- control wave: routing; the shared gate for a shared run
     const bool has_routed = rank0 != a.k;
     if (a.fused_router) {
-      // every workgroup waits for the words, also one with only shared-expert
-      // rows: seeing them orders out's zeros before its atomics
-      double S[NJ], B[NJ];
-      if (poll_router_words<NJ>(a.rtag, a.E, a.epoch, S, B)) {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // out's zeros are visible from here on
-        if (has_routed) {
+      if (has_routed) {
+        double S[NJ], B[NJ];
+        if (poll_router_words<NJ>(a.rtag, a.E, a.epoch, S, B)) {
           const bool ok = certified_select_regs<NJ>(S, B, a.E, a.k, a.scope, writer ? a.ids : nullptr,
                                                     writer ? a.weights : nullptr, s_ids, s_w, -2, s_spec);
           need_exact = !ok;
+        } else {
+          // timed out: flag it for the host (the call's result is not
+          // trustworthy), stream expert 0 tentatively and route this
+          // workgroup with the exact logits so that every wave still finishes
+          if (threadIdx.x == 0) __hip_atomic_store(a.xchg_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          if (threadIdx.x < a.k)
+            __hip_atomic_store(&s_spec[threadIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          need_exact = true;
         }
-      } else {
-        // timed out: flag it for the host (the call's result is not
-        // trustworthy), stream expert 0 tentatively and route this workgroup
-        // with the exact logits so that every wave still finishes
-        if (threadIdx.x == 0) __hip_atomic_store(a.xchg_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        if (has_routed && threadIdx.x < a.k)
-          __hip_atomic_store(&s_spec[threadIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        need_exact = has_routed;
       }
     } else if (has_routed && a.sb) {
       const bool ok = certified_select_nj<NJ>(a.sb + (size_t)t * a.E * 2, a.E, a.k, a.scope,
@@ -592,6 +617,11 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   te0 = run_expert(0, true);
   te1 = nruns > 1 ? run_expert(1, true) : 0;
   process_rows(te0, te1, 3, use_burst);
+  if (ctl && a.fused_router) {
+    // out's zeros, every workgroup's slice, before this workgroup's atomics
+    if (poll_zero_flags(a.ztag, gridDim.x, a.epoch)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    else if (threadIdx.x == 0) __hip_atomic_store(a.xchg_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
   if (threadIdx.x == 0) s_exact = need_exact;
   __syncthreads();  // run sums, s_ids/s_w (when certified), s_sg, s_exact
   if (s_exact) {
@@ -648,19 +678,24 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   }
 }
 
-template <int FMT, int ITER, int NJ>
-static void fused_launch(const FusedArgs &a0, hipStream_t st) {
-  FusedArgs a = a0;
-  // split each token's k*I (+ Is) intermediate rows evenly over about one
-  // wave of blocks per CU, at most kMaxRows rows and two experts per block
+// Splits each token's k*I (+ Is) intermediate rows evenly over about one
+// wave of blocks per CU, at most kMaxRows rows and two experts per block:
+// fills a.rb and a.nb, returns the grid size.
+static int fused_grid(FusedArgs &a) {
   const int U = a.k_routed * a.I + (a.with_shared ? a.Is : 0);
   const int rmax = min(kMaxRows, min(a.k_routed ? a.I : a.Is, a.with_shared ? a.Is : a.I));
   int nb = max(1, (a.n_cu + a.T - 1) / a.T);
   nb = max(nb, (U + rmax - 1) / rmax);
   a.rb = (U + nb - 1) / nb;
   a.nb = (U + a.rb - 1) / a.rb;
+  return a.T * a.nb;
+}
+
+template <int FMT, int ITER, int NJ>
+static void fused_launch(const FusedArgs &a0, hipStream_t st) {
+  FusedArgs a = a0;
+  const int blocks = fused_grid(a);
   a.burst = fused_burst_fits(a.H, a.E);
-  const int blocks = a.T * a.nb;
   const size_t lds = fused_lds_bytes(a.H, a.E);
   // dynamic LDS above 64 KiB has to be allowed per kernel (once per size)
   static size_t allowed = 64 * 1024;
@@ -723,6 +758,13 @@ hipError_t launch_zero(float *p, int64_t n, hipStream_t st) {
 }
 
 hipError_t launch_expert_fused(const FusedArgs &a, hipStream_t st) {
+  if (a.fused_router) {
+    // the in-kernel router needs one expert per wave of waves 1..7 and one
+    // zero flag per workgroup
+    FusedArgs g = a;
+    const int blocks = fused_grid(g);
+    if (a.T != 1 || blocks > kMaxExchangeBlocks || a.E > 7 * blocks) return hipErrorInvalidConfiguration;
+  }
   switch (a.fmt) {
   case kF32: fused_fmt<kF32>(a, st); break;
   case kBF16: fused_fmt<kBF16>(a, st); break;

@@ -93,13 +93,17 @@ struct FusedArgs {
   // T = 1, bf16 router: the kernel computes the router partials itself
   // (fused_router = router chunks per lane, 1, 2 or 4; sb null), exchanges
   // them between its workgroups through rtag (2 words per expert) tagged with
-  // epoch (1..255, a new value every call) and zeroes out itself.  xchg_err
-  // (host-visible) is set if the exchange times out.
+  // epoch (1..255, a new value every call) and zeroes out itself, each
+  // workgroup a slice, announced in ztag (one word per workgroup, at most
+  // kMaxExchangeBlocks).  xchg_err (host-visible) is set if an exchange times
+  // out.
   int fused_router;
   uint64_t *rtag;
+  uint32_t *ztag;
   uint32_t epoch;
   int *xchg_err;
 };
+constexpr int kMaxExchangeBlocks = 4096;
 hipError_t launch_expert_fused(const FusedArgs &a, hipStream_t st);
 bool fused_supported(int fmt, int H, int E);  // the LDS plan fits
 hipError_t launch_zero(float *p, int64_t n, hipStream_t st);

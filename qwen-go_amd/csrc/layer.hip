@@ -439,6 +439,7 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
     l->rtag_epoch = l->rtag_epoch % 255 + 1;
     f.fused_router = rcpl;
     f.rtag = l->rtag;
+    f.ztag = reinterpret_cast<uint32_t *>(l->rtag + 2 * (size_t)E);
     f.epoch = l->rtag_epoch;
     f.xchg_err = l->xchg_err_dev;
   }
@@ -546,7 +547,7 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
   }
   {
     DevBuf b;
-    b.n = (size_t)E * 16;
+    b.n = (size_t)E * 16 + (size_t)kMaxExchangeBlocks * 4;  // router words, then zero flags
     if (hipMalloc(&b.p, b.n) != hipSuccess || hipMemset(b.p, 0, b.n) != hipSuccess) {
       (void)hipGetLastError();
       free_all(l);
