@@ -116,24 +116,26 @@ struct PrefillPlan {
   float *wslot;                 // (slots) routing weight, or the shared gate
   int32_t *slot_of;             // (T, k) slot of each (token, rank)
   int32_t *grp_off, *grp_cnt;   // (E + 1) first slot and slot count per group
-  int32_t *tile_grp, *tile_m0;  // tile table: group and first row of each 256-slot tile
+  int32_t *tile_grp, *tile_m0;  // tile table: group and first row of each tile
   int32_t *n_tiles;             // [0] routed tiles, [1] shared tiles (after the routed ones)
 };
 struct PrefillArgs {
   int T, H, E, k, I, Is, Imax;  // Imax = max(I, Is), the row pitch of act
   int fmt;                      // expert (and shared expert) weight format: BF16, INT8 or INT4
+  int bm;                       // slots per tile, prefill_tile_slots(fmt)
   uint16_t *xb;                 // (T, H) x in bf16
   PrefillPlan p;
-  const uint8_t *gu, *dn;       // gate_up (E, 2I, H); down transposed (E, I, H)
-  const uint16_t *gu_s, *dn_s;
+  const uint8_t *gu, *dn;       // gate_up (E, 2I, H); down in the reference layout (E, H, I)
+  const uint16_t *gu_s, *dn_s;  // scales (E, 2I, H/32) and (E, H, I/32)
   int64_t gu_bytes, gu_scales, dn_bytes, dn_scales;
-  const uint8_t *sgate, *sup, *sdown;
+  const uint8_t *sgate, *sup, *sdown;  // shared: (Is, H), (Is, H), down (H, Is)
   const uint16_t *sgate_s, *sup_s, *sdown_s;
   uint16_t *act;                // (slots, Imax) SwiGLU output, bf16
   float *y;                     // (slots, H) weighted expert outputs
 };
 bool prefill_supported(int expert_fmt, int shared_fmt, int H, int I, int Is);
-int prefill_max_tiles(int T, int k, int E);  // routed tiles, upper bound
+int prefill_tile_slots(int expert_fmt);              // slots per GEMM tile for the format
+int prefill_max_tiles(int T, int k, int E, int bm);  // routed tiles, upper bound
 hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, const float *wts, const float *x,
                                    const float *shared_gate, float *sg, hipStream_t st);
 hipError_t launch_prefill_gate_up(const PrefillArgs &a, bool shared, hipStream_t st);

@@ -49,6 +49,10 @@ struct qmoe_layer {
   int64_t weight_bytes = 0;
 
   DevMat router, gu, dn, sgate, sup, sdown;
+  // down matrices in the reference layout (E, H, I) and (H, Is) as well, for
+  // the batched path (present when it supports the formats)
+  DevMat dnr, sdownr;
+  bool has_ref_down = false;
   float *shared_gate = nullptr;
   bool has_router = false, has_experts = false, has_shared = false;
 
@@ -160,10 +164,19 @@ void free_all(qmoe_layer *l) {
 }
 
 // Moves n stored matrices in the reference layout from device staging into
-// m (at matrix index first), transposing when m is stored transposed.
-qmoe_status place(qmoe_layer *l, const DevMat &m, int64_t first, int64_t n, const uint8_t *src, const uint16_t *ss) {
+// m (at matrix index first), transposing when m is stored transposed; a copy
+// in the reference layout also goes into twin, when given.
+qmoe_status place(qmoe_layer *l, const DevMat &m, int64_t first, int64_t n, const uint8_t *src, const uint16_t *ss,
+                  const DevMat *twin = nullptr) {
   uint8_t *dst = (uint8_t *)m.w + first * m.mat_bytes;
   uint16_t *ds = m.s ? (uint16_t *)m.s + first * m.mat_scales : nullptr;
+  if (twin) {
+    HIP_TRY(l, hipMemcpyAsync((uint8_t *)twin->w + first * twin->mat_bytes, src, (size_t)(twin->mat_bytes * n),
+                              hipMemcpyDeviceToDevice, l->stream), "copy");
+    if (twin->s)
+      HIP_TRY(l, hipMemcpyAsync((uint16_t *)twin->s + first * twin->mat_scales, ss, (size_t)(twin->mat_scales * n) * 2,
+                                hipMemcpyDeviceToDevice, l->stream), "copy");
+  }
   if (m.transposed) {
     HIP_TRY(l, launch_relayout_transpose(m.fmt, src, ss, n, m.rows, m.cols, dst, ds, l->stream), "relayout launch");
   } else {
@@ -175,7 +188,8 @@ qmoe_status place(qmoe_layer *l, const DevMat &m, int64_t first, int64_t n, cons
   return QMOE_OK;
 }
 
-qmoe_status upload(qmoe_layer *l, const DevMat &m, int64_t n_mat, const void *w, const uint16_t *s) {
+qmoe_status upload(qmoe_layer *l, const DevMat &m, int64_t n_mat, const void *w, const uint16_t *s,
+                   const DevMat *twin = nullptr) {
   if (!w) return fail(l, QMOE_ERR_INVALID, "null weight pointer");
   if (fmt_quant(m.fmt) && !s) return fail(l, QMOE_ERR_INVALID, "null scale pointer for a quantised format");
   if (m.transposed) {
@@ -195,7 +209,7 @@ qmoe_status upload(qmoe_layer *l, const DevMat &m, int64_t n_mat, const void *w,
         (void)hipFree(tmp);
         return hip_fail(l, e, "weight upload");
       }
-      qmoe_status st = place(l, m, e0, n, tmp, tsc);
+      qmoe_status st = place(l, m, e0, n, tmp, tsc, twin);
       if (st != QMOE_OK) {
         (void)hipFree(tmp);
         return st;
@@ -253,7 +267,7 @@ constexpr int kMaxGemvTokens = 32;
 
 bool use_mfma(const qmoe_layer *l, int T) {
   const qmoe_desc &d = l->d;
-  return T > kMaxGemvTokens &&
+  return T > kMaxGemvTokens && l->has_ref_down &&
          prefill_supported(d.expert_fmt, d.shared_fmt, d.hidden, d.moe_inter, d.shared_inter);
 }
 
@@ -272,7 +286,8 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_sb = take((size_t)nT * d.n_experts * 16);
   const bool want_mfma = mfma || l->ws_mfma;
   const size_t pairs = (size_t)nT * d.top_k, slots = pairs + (size_t)nT;
-  const size_t tiles = (size_t)prefill_max_tiles(nT, d.top_k, d.n_experts) + (nT + 127) / 128;
+  const int bm = prefill_tile_slots(d.expert_fmt);
+  const size_t tiles = (size_t)prefill_max_tiles(nT, d.top_k, d.n_experts, bm) + (nT + bm - 1) / bm;
   const int imax = std::max(d.moe_inter, d.shared_inter);
   size_t o_xb = 0, o_sg = 0, o_tok = 0, o_wsl = 0, o_slot = 0, o_goff = 0, o_gcnt = 0, o_tg = 0, o_tm = 0,
          o_nt = 0, o_act = 0, o_y = 0;
@@ -351,23 +366,24 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
     pa.Is = Is;
     pa.Imax = std::max(I, Is);
     pa.fmt = d.expert_fmt;
+    pa.bm = prefill_tile_slots(d.expert_fmt);
     pa.xb = l->xb;
     pa.p = l->plan;
     pa.gu = l->gu.w;
-    pa.dn = l->dn.w;
+    pa.dn = l->dnr.w;
     pa.gu_s = l->gu.s;
-    pa.dn_s = l->dn.s;
+    pa.dn_s = l->dnr.s;
     pa.gu_bytes = l->gu.mat_bytes;
     pa.gu_scales = l->gu.mat_scales;
-    pa.dn_bytes = l->dn.mat_bytes;
-    pa.dn_scales = l->dn.mat_scales;
+    pa.dn_bytes = l->dnr.mat_bytes;
+    pa.dn_scales = l->dnr.mat_scales;
     if (Is > 0) {
       pa.sgate = l->sgate.w;
       pa.sup = l->sup.w;
-      pa.sdown = l->sdown.w;
+      pa.sdown = l->sdownr.w;
       pa.sgate_s = l->sgate.s;
       pa.sup_s = l->sup.s;
-      pa.sdown_s = l->sdown.s;
+      pa.sdown_s = l->sdownr.s;
     }
     pa.act = l->act;
     pa.y = l->y;
@@ -533,6 +549,14 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
     delete l;
     return s;
   }
+  l->has_ref_down = prefill_supported(d.expert_fmt, d.shared_fmt, H, I, Is);
+  if (l->has_ref_down && ((s = alloc_mat(l, l->dnr, d.expert_fmt, E, H, I)) != QMOE_OK ||
+                          (Is > 0 && (s = alloc_mat(l, l->sdownr, d.shared_fmt, 1, H, Is)) != QMOE_OK))) {
+    g_create_error = l->err;
+    free_all(l);
+    delete l;
+    return s;
+  }
   {
     DevBuf b;
     b.n = 256;
@@ -617,7 +641,7 @@ qmoe_status qmoe_set_experts(qmoe_layer *l, const void *gate_up, const uint16_t 
   if (s) return s;
   const int E = l->d.n_experts;
   if ((s = upload(l, l->gu, E, gate_up, gate_up_scales)) != QMOE_OK) return s;
-  if ((s = upload(l, l->dn, E, down, down_scales)) != QMOE_OK) return s;
+  if ((s = upload(l, l->dn, E, down, down_scales, l->has_ref_down ? &l->dnr : nullptr)) != QMOE_OK) return s;
   l->has_experts = true;
   return QMOE_OK;
 }
@@ -633,7 +657,7 @@ qmoe_status qmoe_set_shared(qmoe_layer *l, const void *gate, const uint16_t *gat
   if (!shared_gate) return fail(l, QMOE_ERR_INVALID, "null shared_gate");
   if ((s = upload(l, l->sgate, 1, gate, gate_scales)) != QMOE_OK) return s;
   if ((s = upload(l, l->sup, 1, up, up_scales)) != QMOE_OK) return s;
-  if ((s = upload(l, l->sdown, 1, down, down_scales)) != QMOE_OK) return s;
+  if ((s = upload(l, l->sdown, 1, down, down_scales, l->has_ref_down ? &l->sdownr : nullptr)) != QMOE_OK) return s;
   HIP_TRY(l, hipMemcpy(l->shared_gate, shared_gate, (size_t)l->d.hidden * 4, hipMemcpyHostToDevice),
           "shared gate upload");
   l->has_shared = true;
@@ -680,7 +704,7 @@ qmoe_status qmoe_quantize_experts(qmoe_layer *l, const float *gate_up, const flo
         (void)hipFree(tmp);
         return hip_fail(l, err, "expert quantisation");
       }
-      qmoe_status st = place(l, m, e0, n, qc, qs);
+      qmoe_status st = place(l, m, e0, n, qc, qs, which == 1 && l->has_ref_down ? &l->dnr : nullptr);
       if (st != QMOE_OK) {
         (void)hipFree(tmp);
         return st;

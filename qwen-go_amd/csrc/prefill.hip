@@ -9,14 +9,15 @@
 //             range, then a scatter of every pair into its expert's range
 //             (tok[slot], its routing weight, slot_of[t*k + r]).  The shared
 //             expert is group E, owning slots [T*k, T*k + T) in token order.
-//             Also the tile table: one entry per 256 slots of a group.
-//   gate_up   grouped GEMM: per (tile, 64 intermediate columns) a 256 x 128
-//             output block = 256 gathered bf16 rows of x times the expert's
+//             Also the tile table: one entry per 128 slots of a group.
+//   gate_up   grouped GEMM: per (tile, 64 intermediate columns) a 128 x 128
+//             output block = 128 gathered bf16 rows of x times the expert's
 //             gate rows [n0, n0+64) and up rows [I+n0, I+n0+64) over K = H,
 //             on v_mfma_f32_32x32x16_bf16 with f32 accumulation; SwiGLU in the
 //             epilogue (model/moe.go:64-75): act = silu(g) * u, stored bf16.
-//   down      grouped GEMM: act rows of the tile times the expert's down
-//             matrix over K = I; the routing weight (or shared gate) scales
+//   down      grouped GEMM: act rows of the tile times 128 rows of the
+//             expert's down matrix, (H, I) reference layout, over K = I; the
+//             routing weight (or shared gate) scales
 //             the f32 result, y[slot] = w * (down . act) (model/moe.go:76-84).
 //   combine   out[t] = sum over ranks r in rank order of y[slot_of[t, r]],
 //             then + y[shared slot of t] (model/moe.go:82-97).
@@ -25,10 +26,9 @@
 //
 // Expert weights are bf16, or int8 / int4 group-32 codes with fp16 scales
 // that the GEMMs dequantise to bf16 in LDS on the way to the MFMAs.  Tiles are
-// staged through LDS with global_load_lds (16 bytes per lane) in a ring of
-// three stages, an XOR swizzle of the 16-byte chunks of each 128-byte row so
-// that the MFMA operand reads (one row per lane) hit distinct banks.  The
-// down matrices are stored transposed, (I, H), for the decode kernel.
+// staged through LDS with global_load_lds (16 bytes per lane), an XOR swizzle
+// of the 16-byte chunks of each 128-byte row so that the MFMA operand reads
+// (one row per lane) hit distinct banks.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -37,7 +37,6 @@ namespace qmoe {
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
 
-constexpr int kBM = 256;        // slots per tile
 constexpr int kBK = 64;         // K per stage (128 bytes of bf16 per row)
 constexpr int kGemmThreads = 512;
 
@@ -92,7 +91,7 @@ constexpr int kDispatchThreads = 1024;
 
 __global__ void __launch_bounds__(kDispatchThreads)
     dispatch_kernel(const int32_t *__restrict__ ids, const float *__restrict__ wts, const float *__restrict__ sg,
-                    int T, int k, int E, int with_shared, PrefillPlan p) {
+                    int T, int k, int E, int with_shared, int bm, PrefillPlan p) {
   __shared__ int cnt[1024], incl[1024], tincl[1024], cur[1024];
   const int tid = threadIdx.x;
   const int n = T * k;
@@ -102,7 +101,7 @@ __global__ void __launch_bounds__(kDispatchThreads)
   __syncthreads();
   // inclusive scans of the counts and of the tiles per expert (E <= 1024)
   const int c = tid < E ? cnt[tid] : 0;
-  const int ct = (c + kBM - 1) / kBM;
+  const int ct = (c + bm - 1) / bm;
   incl[tid] = c;
   tincl[tid] = ct;
   __syncthreads();
@@ -122,13 +121,13 @@ __global__ void __launch_bounds__(kDispatchThreads)
     cur[tid] = off;
     for (int q = 0; q < ct; q++) {
       p.tile_grp[toff + q] = tid;
-      p.tile_m0[toff + q] = q * kBM;
+      p.tile_m0[toff + q] = q * bm;
     }
   }
-  const int shared_tiles = with_shared ? (T + kBM - 1) / kBM : 0;
+  const int shared_tiles = with_shared ? (T + bm - 1) / bm : 0;
   for (int q = tid; q < shared_tiles; q += kDispatchThreads) {
     p.tile_grp[routed_tiles + q] = E;
-    p.tile_m0[routed_tiles + q] = q * kBM;
+    p.tile_m0[routed_tiles + q] = q * bm;
   }
   if (tid == 0) {
     p.n_tiles[0] = routed_tiles;
@@ -157,7 +156,7 @@ struct TileInfo {
   bool ok;
 };
 
-__device__ __forceinline__ TileInfo tile_of(const PrefillPlan &p, int E, bool shared_launch, int tile) {
+__device__ __forceinline__ TileInfo tile_of(const PrefillPlan &p, int E, bool shared_launch, int tile, int bm) {
   TileInfo ti{0, 0, 0, false};
   const int nt = shared_launch ? p.n_tiles[1] : p.n_tiles[0];
   if (tile >= nt) return ti;
@@ -165,51 +164,60 @@ __device__ __forceinline__ TileInfo tile_of(const PrefillPlan &p, int E, bool sh
   ti.g = p.tile_grp[idx];
   const int m0 = p.tile_m0[idx];
   ti.slot0 = p.grp_off[ti.g] + m0;
-  ti.rows = min(kBM, p.grp_cnt[ti.g] - m0);
+  ti.rows = min(bm, p.grp_cnt[ti.g] - m0);
   ti.ok = ti.g <= E && ti.rows > 0;
   return ti;
 }
 
 // ----------------------------------------------------------- grouped GEMM
 //
-// One workgroup: 256 slots x 128 output columns, 8 waves; wave w owns slots
-// [64 (w & 3), +64) and half of the columns (w >> 2).  K advances 64 at a time
-// through a ring of 3 LDS stages filled by global_load_lds two steps ahead.
-//   A stage: 256 rows x 128 bytes (bf16 rows of x, or of act), chunk-swizzled.
-//   B stage (gate_up): 128 weight rows x 128 bytes -- gate rows [n0, n0+64)
-//            then up rows [I+n0, I+n0+64) -- chunk-swizzled like A.
-//   B stage (down):    64 K rows x 256 bytes of the (I, H) down matrix
-//            (128 columns); a lane gathers its 8 K values of one column with
-//            8 two-byte LDS reads.  Chunks are XOR-ed with 4 in K rows 8..15
-//            of every 16 so that the two half-waves hit different banks.
+// One workgroup: a tile of BM slots (256 for bf16 weights, 128 for the
+// group-32 formats) x 256 B rows over K, 8 waves in 4 x 2: wave w owns the
+// slots [BM/4 (w >> 1), +BM/4) and half of the B rows (w & 1) -- for gate_up
+// the gate rows [n0 + 64 (w & 1), +64) and the up rows with the same
+// indices, so that a SwiGLU pair stays in one wave; for down 128 output
+// columns.  B is always a matrix with its rows along K: gate and up rows of
+// the (2I, H) stack, or rows of the down matrix in the reference (H, I)
+// layout, which the device keeps next to the decode kernel's transposed copy.
 //
-// INT8 / INT4 group-32 experts (model/moe.go:124-157): the stage holds the B
-// codes (the same 64 K x 128 columns, 1 or 0.5 byte each) and their fp16
-// scales, loaded by global_load_lds like the rest.  Each wave then dequantises
-// the code pieces it loaded itself, w = code * scale (the f32 product of
-// quantLinear.dequantize) rounded to bf16, into a bf16 B tile laid out as
-// above (two such tiles alternate).  Since a wave converts only its own
+// Large tiles keep the bytes that cross the L2 per MFMA low: every K step
+// brings BM + 256 rows of 128 bytes into LDS for BM x 256 x 64 multiply-adds.
+// K advances 64 at a time.  A (BM x 64 bf16: gathered rows of x, or act) and
+// B (256 x 64: bf16, or int8 / int4 codes plus their scales) come into LDS
+// by global_load_lds on rings of their own.  Rows are 128 bytes with an XOR
+// swizzle of their 16-byte chunks so that the MFMA operand reads (one row per
+// lane) hit distinct banks.
+//
+// INT8 / INT4 group-32 experts (model/moe.go:124-157): each thread
+// dequantises the code pieces it loaded itself, w = code * scale (the f32
+// product of quantLinear.dequantize) rounded to bf16, into a bf16 B tile (two
+// alternate) before the step's barrier; since a wave converts only its own
 // loads, its own wait for them suffices and a K step keeps one barrier.
 
 enum GemmKind { kGateUp = 0, kDown = 1 };
 
 constexpr int kWaves = kGemmThreads / 64;
-constexpr int kAStage = kBM * kBK * 2;          // 32 KB
-constexpr int kBStage = 128 * kBK * 2;          // 16 KB (bf16 B tile)
-constexpr int kADma = kAStage / 16 / kGemmThreads;  // 16-byte pieces per thread per stage
-constexpr int kBDma = kBStage / 16 / kGemmThreads;
+constexpr int kBN = 256;                        // B rows per tile
+constexpr int kBStage = kBN * kBK * 2;          // 32 KB (bf16 B tile)
 
-// LDS plan of a B format.
+// Tile and LDS plan of a weight format.
 template <int BF>
-struct BGeom {
+struct GemmCfg {
   static constexpr bool kQuant = BF == kINT8 || BF == kINT4;
+  static constexpr int kBM = kQuant ? 128 : 256;                    // slots per tile
+  static constexpr int kAStage = kBM * kBK * 2;
+  static constexpr int kADma = kAStage / 16 / kGemmThreads;         // A pieces per thread per step
+  static constexpr int kAStages = kQuant ? (BF == kINT8 ? 2 : 3) : 2;  // A ring: kAStages - 1 steps ahead
   static constexpr int kPieceElems = BF == kINT8 ? 16 : 32;         // elements per 16-byte code piece
-  static constexpr int kRaw = 128 * kBK * fmt_bytes_x2(BF) / 2;     // code bytes per stage
-  static constexpr int kBWaves = kQuant ? kRaw / 16 / 64 : kWaves;  // waves that load (and convert) B
-  static constexpr int kScale = kBWaves * 256;                      // fp16 scales per stage, 256 B per wave
-  static constexpr int kStage = kAStage + (kQuant ? kRaw + kScale : kBStage);
+  static constexpr int kRaw = kBN * kBK * fmt_bytes_x2(BF) / 2;     // B bytes per stage (codes, or bf16)
+  static constexpr int kBPieces = kRaw / 16 / kGemmThreads;         // B pieces per thread per step
+  static constexpr int kScale = kQuant ? kBPieces * kGemmThreads * 4 : 0;  // a scale dword per code piece
+  static constexpr int kBSize = kRaw + kScale;                      // one B ring stage
+  static constexpr int kBStages = kQuant ? (BF == kINT8 ? 2 : 3) : 2;  // B ring: kBStages - 1 steps ahead
   static constexpr int kTile = kQuant ? kBStage : 16;               // one dequantised B tile
-  static constexpr int kBLoads = kQuant ? 2 : kBDma;                // B loads per B-wave thread per step
+  static constexpr int kBLoads = kQuant ? 2 * kBPieces : kBPieces;  // B loads per thread per step
+  static constexpr int kRB = kBM / 4;                               // slots per wave
+  static constexpr int kNRB = kRB / 32;                             // 32-slot blocks per wave
 };
 
 // s_waitcnt vmcnt(N) with the other counters untouched (gfx9 encoding).  The
@@ -252,37 +260,33 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return r;
 }
 
-// Dequantised values of one 16-byte code piece, as packed bf16 pairs:
-// out[i] holds elements 2i and 2i+1.  scale(e) gives element e's scale.
-// INT8: 16 codes, value = code.  INT4: 32 elements, byte b holds element 2b in
-// its high nibble and 2b+1 in its low nibble, value = nibble - 8; the product
-// (nibble - 8) * s is formed as fma(nibble, s, -8 s), which rounds the same
-// exact value once.
-template <int BF, typename ScaleFn>
-__device__ __forceinline__ void dequant_piece(const uint4 v, ScaleFn scale,
-                                              uint32_t (&out)[BGeom<BF>::kPieceElems / 2]) {
+// Dequantised values of one 16-byte code piece with one scale s, as packed
+// bf16 pairs: out[i] holds elements 2i and 2i+1.  INT8: 16 codes, value =
+// code.  INT4: 32 elements, byte b holds element 2b in its high nibble and
+// 2b+1 in its low nibble, value = nibble - 8; the product (nibble - 8) * s is
+// formed as fma(nibble, s, -8 s), which rounds the same exact value once.
+template <int BF>
+__device__ __forceinline__ void dequant_piece(const uint4 v, float s, uint32_t (&out)[GemmCfg<BF>::kPieceElems / 2]) {
   const uint32_t u[4] = {v.x, v.y, v.z, v.w};
   if constexpr (BF == kINT8) {
 #pragma unroll
     for (int q = 0; q < 4; q++)
 #pragma unroll
       for (int b = 0; b < 4; b += 2) {
-        const int e = 4 * q + b;
-        const float f0 = (float)(int8_t)((u[q] >> (8 * b)) & 0xffu) * scale(e);
-        const float f1 = (float)(int8_t)((u[q] >> (8 * b + 8)) & 0xffu) * scale(e + 1);
-        out[e / 2] = pack_bf16(f0, f1);
+        const float f0 = (float)(int8_t)((u[q] >> (8 * b)) & 0xffu) * s;
+        const float f1 = (float)(int8_t)((u[q] >> (8 * b + 8)) & 0xffu) * s;
+        out[(4 * q + b) / 2] = pack_bf16(f0, f1);
       }
   } else {
+    const float m8 = -8.0f * s;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const uint32_t hi = (u[q] >> 4) & 0x0f0f0f0fu, lo = u[q] & 0x0f0f0f0fu;
 #pragma unroll
       for (int b = 0; b < 4; b++) {
-        const int e = 8 * q + 2 * b;
-        const float s0 = scale(e), s1 = scale(e + 1);
-        const float f0 = fmaf((float)((hi >> (8 * b)) & 0xffu), s0, -8.0f * s0);
-        const float f1 = fmaf((float)((lo >> (8 * b)) & 0xffu), s1, -8.0f * s1);
-        out[e / 2] = pack_bf16(f0, f1);
+        const float f0 = fmaf((float)((hi >> (8 * b)) & 0xffu), s, m8);
+        const float f1 = fmaf((float)((lo >> (8 * b)) & 0xffu), s, m8);
+        out[4 * q + b] = pack_bf16(f0, f1);
       }
     }
   }
@@ -296,255 +300,226 @@ __device__ __forceinline__ void dma4(const void *src, const unsigned char *lds_w
 }
 
 // Work order, XCD-aware: workgroups are dealt to the 8 XCDs round-robin by
-// linear id, so id -> (tile, column chunk) gives every XCD whole tiles and runs
-// the ny column chunks of a tile back to back on one XCD, whose L2 then holds
-// the tile's A rows (gathered x, or act) for all of them.
+// linear id.  XCD x runs the x-th contiguous range of tiles -- tiles of one
+// expert are adjacent, so an expert's B rows come from HBM about once into that
+// XCD's L2 -- and the ny column chunks of a tile back to back, which share the
+// tile's A rows in the same L2.
 constexpr int kXcds = 8;
 
 template <int KIND, int BF>
 __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int shared_launch, int ny) {
-  using G = BGeom<BF>;
-  __shared__ __align__(16) unsigned char lds0[G::kStage], lds1[G::kStage], lds2[G::kStage];
+  using G = GemmCfg<BF>;
+  constexpr int NAS = G::kAStages, DA = NAS - 1;  // A ring stages, A prefetch distance
+  constexpr int NBS = G::kBStages, DB = NBS - 1;  // B ring stages, B prefetch distance
+  __shared__ __align__(16) unsigned char aring[NAS][G::kAStage];
+  __shared__ __align__(16) unsigned char bring[NBS][G::kBSize];
   __shared__ __align__(16) unsigned char btile[2][G::kTile];
   const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
-  const int tile = (j / ny) * kXcds + xcd, chunk = j % ny;
-  const TileInfo ti = tile_of(a.p, a.E, shared_launch, tile);
+  const int nt = shared_launch ? a.p.n_tiles[1] : a.p.n_tiles[0];
+  const int per_xcd = (nt + kXcds - 1) / kXcds;
+  const int local = j / ny, chunk = j % ny;
+  if (local >= per_xcd) return;
+  const TileInfo ti = tile_of(a.p, a.E, shared_launch, xcd * per_xcd + local, G::kBM);
   if (!ti.ok) return;
   const bool sh = ti.g == a.E;
   const int H = a.H;
-  const int N = KIND == kGateUp ? (sh ? a.Is : a.I) : H;       // output columns of the group
-  const int K = KIND == kGateUp ? H : (sh ? a.Is : a.I);
-  const int n0 = chunk * (KIND == kGateUp ? 64 : 128);
+  const int Ig = sh ? a.Is : a.I;                  // intermediate size of the group
+  const int N = KIND == kGateUp ? Ig : H;          // output columns of the group
+  const int K = KIND == kGateUp ? H : Ig;
+  const int n0 = chunk * (KIND == kGateUp ? kBN / 2 : kBN);
   if (n0 >= N) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, so branches on it are scalar
-  const int64_t rb = fmt_matrix_bytes(BF, 1, H);  // bytes of a gate/up row or of a transposed down row
+  const int64_t rbB = fmt_matrix_bytes(BF, 1, K);         // bytes of one B row
+  const int gsc = K / kGroup;                             // scales per B row
+
+  // B row r of the tile and its scale row: gate_up rows n0 + r (gate,
+  // r < 128) or up rows n0 + r - 128; down rows n0 + r of the (H, K) matrix
+  auto brow = [&](int r, const uint16_t *&srow) -> const uint8_t * {
+    srow = nullptr;
+    if constexpr (KIND == kGateUp) {
+      const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)ti.g * a.gu_bytes;
+      const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * rbB;
+      const int row = r < kBN / 2 ? n0 + r : n0 + r - kBN / 2;
+      if constexpr (G::kQuant) {
+        const uint16_t *gs = sh ? a.sgate_s : a.gu_s + (size_t)ti.g * a.gu_scales;
+        const uint16_t *us = sh ? a.sup_s : gs + (size_t)a.I * gsc;
+        srow = (r < kBN / 2 ? gs : us) + (size_t)row * gsc;
+      }
+      return (r < kBN / 2 ? gb : ub) + (size_t)row * rbB;
+    } else {
+      const uint8_t *db = sh ? a.sdown : a.dn + (size_t)ti.g * a.dn_bytes;
+      if constexpr (G::kQuant) srow = (sh ? a.sdown_s : a.dn_s + (size_t)ti.g * a.dn_scales) + (size_t)(n0 + r) * gsc;
+      return db + (size_t)(n0 + r) * rbB;
+    }
+  };
 
   // A rows staged by this thread: row r = (i * kWaves + w) * 8 + lane / 8
-  const uint16_t *arow[kADma];
-  int achunk[kADma];
+  const uint16_t *arow[G::kADma];
+  int achunk[G::kADma];
 #pragma unroll
-  for (int i = 0; i < kADma; i++) {
+  for (int i = 0; i < G::kADma; i++) {
     const int r = (i * kWaves + w) * 8 + (lane >> 3);
     achunk[i] = (lane & 7) ^ swz_of(r);
     const int m = min(r, ti.rows - 1);
     if constexpr (KIND == kGateUp) arow[i] = a.xb + (size_t)a.p.tok[ti.slot0 + m] * H;
     else arow[i] = a.act + (size_t)(ti.slot0 + m) * a.Imax;
   }
-  // B pieces staged by this thread (bf16), or its code piece and scale
-  // source (INT formats, waves below kBWaves)
-  const uint16_t *bsrc[kBDma];
-  const uint8_t *qsrc = nullptr;   // code piece at K step 0
-  const uint16_t *ssrc = nullptr;  // scales at K step 0
-  const bool bwave = G::kBWaves == kWaves || w < G::kBWaves;
-  if constexpr (!G::kQuant) {
+  // B pieces staged by this thread: piece i is 16-byte slot (i * kWaves + w)
+  // * 64 + lane of the stage.  bf16: row r = slot / 8, its chunk swizzled;
+  // INT formats: row r = slot / PPR, K elements [p * PE, +PE) of the step,
+  // plus the dword of the row's two scales of the step.
+  const uint8_t *bsrc[G::kBPieces];
+  const uint16_t *ssrc[G::kBPieces];
 #pragma unroll
-    for (int i = 0; i < kBDma; i++) {
-      const int sidx = (i * kWaves + w) * 64 + lane;  // 16-byte slot of the stage
-      if constexpr (KIND == kGateUp) {
-        const int r = sidx >> 3, c = (sidx & 7) ^ swz_of(r);
-        const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)ti.g * a.gu_bytes;
-        const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * rb;
-        const uint8_t *row = r < 64 ? gb + (size_t)(n0 + r) * rb : ub + (size_t)(n0 + r - 64) * rb;
-        bsrc[i] = reinterpret_cast<const uint16_t *>(row) + c * 8;
-      } else {
-        const int kr = sidx >> 4, c = (sidx & 15) ^ (((kr >> 3) & 1) << 2);
-        const uint8_t *db = sh ? a.sdown : a.dn + (size_t)ti.g * a.dn_bytes;
-        bsrc[i] = reinterpret_cast<const uint16_t *>(db) + (size_t)kr * H + n0 + c * 8;
-      }
-    }
-  } else if (bwave) {
-    const int gsc = H / kGroup;  // scales per gate/up row
-    if constexpr (KIND == kGateUp) {
-      // piece tid: row r, K elements [p * PE, +PE) of the stage
-      constexpr int PPR = kBK / G::kPieceElems;
-      const int r = tid / PPR, p = tid % PPR;
-      const uint8_t *gb = sh ? a.sgate : a.gu + (size_t)ti.g * a.gu_bytes;
-      const uint8_t *ub = sh ? a.sup : gb + (size_t)a.I * rb;
-      const uint16_t *gs = sh ? a.sgate_s : a.gu_s + (size_t)ti.g * a.gu_scales;
-      const uint16_t *us = sh ? a.sup_s : gs + (size_t)a.I * gsc;
-      const int row = r < 64 ? n0 + r : n0 + r - 64;
-      qsrc = (r < 64 ? gb : ub) + (size_t)row * rb + p * 16;
-      ssrc = (r < 64 ? gs : us) + (size_t)row * gsc;  // + 2 kt: the row's two groups of the step
+  for (int i = 0; i < G::kBPieces; i++) {
+    const int sidx = (i * kWaves + w) * 64 + lane;
+    if constexpr (!G::kQuant) {
+      const int r = sidx >> 3, c = (sidx & 7) ^ swz_of(r);
+      bsrc[i] = brow(r, ssrc[i]) + c * 16;
     } else {
-      // piece tid: K row kr, columns [n0 + p * PE, +PE); lanes 0..15 load the
-      // wave's 128 column scales of its group
-      constexpr int PPR = 128 / G::kPieceElems;
-      const int kr = tid / PPR, p = tid % PPR;
-      const uint8_t *db = sh ? a.sdown : a.dn + (size_t)ti.g * a.dn_bytes;
-      const uint16_t *ds = sh ? a.sdown_s : a.dn_s + (size_t)ti.g * a.dn_scales;
-      qsrc = db + (size_t)kr * rb + (size_t)n0 * fmt_bytes_x2(BF) / 2 + p * 16;
-      ssrc = ds + n0 + (lane & 15) * 8;  // + ((k0 + first K row of the wave) / 32) * H
+      constexpr int PPR = kBK / G::kPieceElems;
+      bsrc[i] = brow(sidx / PPR, ssrc[i]) + (sidx % PPR) * 16;
     }
   }
-  auto issue = [&](unsigned char *sa, int kt) {
-    const int k0 = kt * kBK;
+  // loads of step s (slot by s, source clamped to the last step: past the end
+  // of K a step re-reads the last K slice into a slot never read again, so
+  // every step issues the same number of loads)
+  const int KT = K / kBK;
+  auto issue_a = [&](int s) {
+    unsigned char *dst = aring[s % NAS];
+    const int k0 = min(s, KT - 1) * kBK;
 #pragma unroll
-    for (int i = 0; i < kADma; i++) dma16(arow[i] + k0 + achunk[i] * 8, sa + (i * kWaves + w) * 1024);
-    if constexpr (!G::kQuant) {
-      unsigned char *sb = sa + kAStage;
+    for (int i = 0; i < G::kADma; i++) dma16(arow[i] + k0 + achunk[i] * 8, dst + (i * kWaves + w) * 1024);
+  };
+  auto issue_b = [&](int s) {
+    unsigned char *dst = bring[s % NBS];
+    const int kt = min(s, KT - 1);
 #pragma unroll
-      for (int i = 0; i < kBDma; i++) {
-        const uint16_t *src = KIND == kGateUp ? bsrc[i] + k0 : bsrc[i] + (size_t)k0 * H;
-        dma16(src, sb + (i * kWaves + w) * 1024);
-      }
-    } else if (bwave) {
-      unsigned char *raw = sa + kAStage, *sc = raw + G::kRaw;
-      if constexpr (KIND == kGateUp) {
-        dma16(qsrc + (size_t)k0 * fmt_bytes_x2(BF) / 2, raw + w * 1024);
-        dma4(ssrc + 2 * kt, sc + w * 256);
-      } else {
-        dma16(qsrc + (size_t)k0 * rb, raw + w * 1024);
-        constexpr int RPW = 64 / G::kBWaves;  // K rows per wave
-        if (lane < 16) dma16(ssrc + (size_t)((k0 + w * RPW) / kGroup) * H, sc + w * 256);
-      }
+    for (int i = 0; i < G::kBPieces; i++) {
+      dma16_nt(bsrc[i] + (size_t)kt * kBK * fmt_bytes_x2(BF) / 2, dst + (i * kWaves + w) * 1024);
+      if constexpr (G::kQuant) dma4(ssrc[i] + 2 * kt, dst + G::kRaw + (i * kWaves + w) * 256);
     }
   };
-  // INT formats: dequantise this wave's code pieces of stage `cur` into `bt`
-  auto convert = [&](const unsigned char *cur, unsigned char *bt) {
+  // INT formats: dequantise this thread's code pieces of a stage into `bt`
+  auto convert = [&](const unsigned char *stage, unsigned char *bt) {
     if constexpr (G::kQuant) {
-      if (!bwave) return;
-      constexpr int PE = G::kPieceElems;
-      const unsigned char *raw = cur + kAStage, *sc = raw + G::kRaw + w * 256;
-      const uint4 v = *reinterpret_cast<const uint4 *>(raw + tid * 16);
-      uint32_t o[PE / 2];
-      if constexpr (KIND == kGateUp) {
-        constexpr int PPR = kBK / PE;
-        const int r = tid / PPR, p = tid % PPR;
-        const uint32_t sw = *reinterpret_cast<const uint32_t *>(sc + lane * 4);
+      constexpr int PE = G::kPieceElems, PPR = kBK / PE;
+#pragma unroll
+      for (int i = 0; i < G::kBPieces; i++) {
+        const int sidx = (i * kWaves + w) * 64 + lane;
+        const int r = sidx / PPR, p = sidx % PPR;
+        const uint4 v = *reinterpret_cast<const uint4 *>(stage + sidx * 16);
+        const uint32_t sw = *reinterpret_cast<const uint32_t *>(stage + G::kRaw + sidx * 4);
         const float s = f16_to_f32((uint16_t)(((p * PE) / kGroup) ? (sw >> 16) : (sw & 0xffffu)));
-        dequant_piece<BF>(v, [&](int) { return s; }, o);
+        uint32_t o[PE / 2];
+        dequant_piece<BF>(v, s, o);
 #pragma unroll
         for (int c = 0; c < PE / 8; c++)
           *reinterpret_cast<uint4 *>(bt + swz(r, p * (PE / 8) + c)) =
-              make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
-      } else {
-        constexpr int PPR = 128 / PE;
-        const int kr = tid / PPR, p = tid % PPR;
-        uint4 sv[PE / 8];
-#pragma unroll
-        for (int c = 0; c < PE / 8; c++) sv[c] = *reinterpret_cast<const uint4 *>(sc + (p * PE + 8 * c) * 2);
-        dequant_piece<BF>(v, [&](int e) {
-          const uint32_t word = (&sv[e / 8].x)[(e % 8) / 2];
-          return f16_to_f32((uint16_t)((e & 1) ? (word >> 16) : (word & 0xffffu)));
-        }, o);
-        const int x = ((kr >> 3) & 1) << 2;
-#pragma unroll
-        for (int c = 0; c < PE / 8; c++)
-          *reinterpret_cast<uint4 *>(bt + kr * 256 + (((p * (PE / 8) + c) ^ x) << 4)) =
               make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
       }
       wait_lds_writes();  // the tile is read by every wave after the barrier
     }
   };
 
-  // wave w: slot rows [64 (w >> 1), +64), column half w & 1.  The SIMD of
-  // wave w also runs wave w + 4, whose rows lie 128 further: a tile with few
-  // rows still keeps every SIMD's MFMA busy, and 32-row blocks past the tile's
-  // rows skip their LDS reads and MFMAs.
   const int wm = w >> 1, wn = w & 1, hi = lane >> 5, l32 = lane & 31;
-  const int nb = min(2, max(0, (ti.rows - wm * 64 + 31) >> 5));  // live 32-row blocks of this wave
-  f32x16_t acc[2][2];  // [slot block][gate/up, or column block]
+  // live 32-slot blocks of this wave
+  const int nrb = min(G::kNRB, max(0, (ti.rows - wm * G::kRB + 31) >> 5));
+  f32x16_t acc[G::kNRB][4];  // [slot block][gate 0, gate 1, up 0, up 1 -- or 4 column blocks]
 #pragma unroll
-  for (int b = 0; b < 2; b++)
+  for (int b = 0; b < G::kNRB; b++)
 #pragma unroll
-    for (int q = 0; q < 2; q++)
+    for (int q = 0; q < 4; q++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[b][q][e] = 0.0f;
+  int brl[4];  // this lane's B rows (MFMA columns)
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    brl[q] = KIND == kGateUp ? (q >> 1) * (kBN / 2) + wn * 64 + (q & 1) * 32 + l32 : wn * 128 + q * 32 + l32;
+  const int ar0 = wm * G::kRB + l32;
 
-  const int KT = K / kBK;
-  const int ar0 = wm * 64 + l32;
-  // one K step on stage `cur`; refills stage `nxt2` with step kt + 2
-  // Every step issues one batch of loads, so that the count of loads in flight
-  // is the same at every step: past the end of K the batch re-reads the last K
-  // slice into a stage that is never read again.
-  auto step = [&](const unsigned char *cur, unsigned char *nxt2, int kt) {
-    // stage kt landed; the batch of step kt + 1 may still fly
-    if (!G::kQuant || bwave) wait_vm<kADma + G::kBLoads>();
-    else wait_vm<kADma>();
+  // prologue: the loads of the steps before 0, in the steady-state order
+  // (step s issues A of s + DA, then B of s + DB)
+  constexpr int D = DA > DB ? DA : DB;
+#pragma unroll
+  for (int s = -D; s < 0; s++) {
+    if (s + DA >= 0) issue_a(s + DA);
+    if (s + DB >= 0) issue_b(s + DB);
+  }
+  // At step kt the loads issued after A (or B) of kt, whichever came later,
+  // may still fly: those of the steps after it, and B (A) of its own step.
+  constexpr int kAfterA = (DA - 1) * G::kADma + DA * G::kBLoads;  // A of kt was issued at step kt - DA
+  constexpr int kAfterB = (DB - 1) * (G::kADma + G::kBLoads);     // B of kt at step kt - DB, after its A
+  constexpr int kWait = kAfterA < kAfterB ? kAfterA : kAfterB;
+  for (int kt = 0; kt < KT; kt++) {
+    wait_vm<kWait>();
+    const unsigned char *sa = aring[kt % NAS];
+    const unsigned char *sbs = bring[kt % NBS];
     unsigned char *bt = btile[kt & 1];
-    convert(cur, bt);
-    lds_barrier();  // stage kt visible to all; stage kt + 2 (read at kt - 1) is free
-    const unsigned char *sa = cur, *sb = G::kQuant ? bt : cur + kAStage;
-    bf16x8_t av[2][4], bv[2][4];
-    if (nb == 0) {  // nothing to multiply: keep the pipeline's loads in step
-      issue(nxt2, min(kt + 2, KT - 1));
-      return;
-    }
+    convert(sbs, bt);
+    lds_barrier();  // stage kt visible to all; the slots refilled below were read at kt - 1
+    const unsigned char *sb = G::kQuant ? bt : sbs;
+    bf16x8_t av[G::kNRB][4], bv[4][4];
+    if (nrb > 0) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-      const int c = ks * 2 + hi;
+      for (int ks = 0; ks < 4; ks++) {
+        const int c = ks * 2 + hi;
 #pragma unroll
-      for (int b = 0; b < 2; b++)
-        if (b < nb) av[b][ks] = *reinterpret_cast<const bf16x8_t *>(sa + swz(ar0 + 32 * b, c));
-      if constexpr (KIND == kGateUp) {
-        bv[0][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(wn * 32 + l32, c));
-        bv[1][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(64 + wn * 32 + l32, c));
-      } else {
+        for (int b = 0; b < G::kNRB; b++)
+          if (b < nrb) av[b][ks] = *reinterpret_cast<const bf16x8_t *>(sa + swz(ar0 + 32 * b, c));
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-          const int nl = wn * 64 + q * 32 + l32;
-          const unsigned char *col = sb + (((nl >> 3) ^ (hi << 2)) << 4) + (nl & 7) * 2 + (ks * 16 + hi * 8) * 256;
-          union {
-            uint16_t h[8];
-            bf16x8_t v;
-          } u;
-#pragma unroll
-          for (int i = 0; i < 8; i++) u.h[i] = *reinterpret_cast<const uint16_t *>(col + i * 256);
-          bv[q][ks] = u.v;
-        }
+        for (int q = 0; q < 4; q++) bv[q][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(brl[q], c));
       }
     }
-    issue(nxt2, min(kt + 2, KT - 1));
+    issue_a(kt + DA);
+    issue_b(kt + DB);
+    if (nrb > 0) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++)
+      for (int ks = 0; ks < 4; ks++)
 #pragma unroll
-      for (int b = 0; b < 2; b++)
-        if (b < nb)
+        for (int b = 0; b < G::kNRB; b++)
+          if (b < nrb)
 #pragma unroll
-          for (int q = 0; q < 2; q++)
-            acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b][ks], bv[q][ks], acc[b][q], 0, 0, 0);
-  };
-  issue(lds0, 0);
-  issue(lds1, min(1, KT - 1));
-  for (int kt = 0; kt < KT; kt += 3) {
-    step(lds0, lds2, kt);
-    if (kt + 1 < KT) step(lds1, lds0, kt + 1);
-    if (kt + 2 < KT) step(lds2, lds1, kt + 2);
+            for (int q = 0; q < 4; q++)
+              acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b][ks], bv[q][ks], acc[b][q], 0, 0, 0);
+    }
   }
   wait_vm<0>();  // no LDS-direct load may land after the workgroup ends
 
   if constexpr (KIND == kGateUp) {
     // act = silu(g) * u -> bf16 (model/moe.go:64-75), row pitch Imax
-    const int n = n0 + wn * 32 + l32;
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+    for (int b = 0; b < G::kNRB; b++)
 #pragma unroll
-      for (int j = 0; j < 4; j++)
+      for (int j4 = 0; j4 < 4; j4++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int m = wm * 64 + b * 32 + 8 * j + 4 * hi + i;
+          const int m = wm * G::kRB + b * 32 + 8 * j4 + 4 * hi + i;
           if (m < ti.rows) {
-            const float g = acc[b][0][4 * j + i], u = acc[b][1][4 * j + i];
-            const float sgl = g / (1.0f + __expf(-g));
-            a.act[(size_t)(ti.slot0 + m) * a.Imax + n] = f32_to_bf16_rne(sgl * u);
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+              const float g = acc[b][q][4 * j4 + i], u = acc[b][q + 2][4 * j4 + i];
+              const float sgl = g / (1.0f + __expf(-g));
+              a.act[(size_t)(ti.slot0 + m) * a.Imax + n0 + wn * 64 + q * 32 + l32] = f32_to_bf16_rne(sgl * u);
+            }
           }
         }
   } else {
     // y[slot] = routing weight (or shared gate) * (down . act), f32
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+    for (int b = 0; b < G::kNRB; b++)
 #pragma unroll
-      for (int j = 0; j < 4; j++)
+      for (int j4 = 0; j4 < 4; j4++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int m = wm * 64 + b * 32 + 8 * j + 4 * hi + i;
+          const int m = wm * G::kRB + b * 32 + 8 * j4 + 4 * hi + i;
           if (m < ti.rows) {
             const int slot = ti.slot0 + m;
             const float ws = a.p.wslot[slot];
 #pragma unroll
-            for (int q = 0; q < 2; q++)
-              a.y[(size_t)slot * H + n0 + wn * 64 + q * 32 + l32] = ws * acc[b][q][4 * j + i];
+            for (int q = 0; q < 4; q++)
+              a.y[(size_t)slot * H + n0 + wn * 128 + q * 32 + l32] = ws * acc[b][q][4 * j4 + i];
           }
         }
   }
@@ -579,15 +554,24 @@ __global__ void __launch_bounds__(256) combine_kernel(const float *__restrict__ 
 // ------------------------------------------------------------- launchers
 
 bool prefill_supported(int expert_fmt, int shared_fmt, int H, int I, int Is) {
-  // bf16, int8 or int4 experts; the shared expert (if any) in the same format
+  // bf16, int8 or int4 experts; the shared expert (if any) in the same format;
+  // whole column chunks (gate_up: 128 intermediate columns, down: 256 outputs)
   if (expert_fmt != kBF16 && expert_fmt != kINT8 && expert_fmt != kINT4) return false;
   if (Is > 0 && shared_fmt != expert_fmt) return false;
-  return H % 128 == 0 && I % 64 == 0 && (Is == 0 || Is % 64 == 0);
+  return H % kBN == 0 && I % (kBN / 2) == 0 && (Is == 0 || Is % (kBN / 2) == 0);
 }
 
-int prefill_max_tiles(int T, int k, int E) {
+int prefill_tile_slots(int expert_fmt) {
+  switch (expert_fmt) {
+  case kINT8: return GemmCfg<kINT8>::kBM;
+  case kINT4: return GemmCfg<kINT4>::kBM;
+  default: return GemmCfg<kBF16>::kBM;
+  }
+}
+
+int prefill_max_tiles(int T, int k, int E, int bm) {
   const int n = T * k;
-  return (n + kBM - 1) / kBM + (E < n ? E : n);
+  return (n + bm - 1) / bm + (E < n ? E : n);
 }
 
 hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, const float *wts, const float *x,
@@ -596,14 +580,15 @@ hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, con
   QMOE_LAUNCH(prep_kernel, dim3(a.T), dim3(256), 0, st, x, a.H, with_shared ? shared_gate : nullptr, a.xb,
                      sg);
   QMOE_LAUNCH(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, st, ids, wts, sg, a.T, a.k, a.E,
-                     (int)with_shared, a.p);
+                     (int)with_shared, a.bm, a.p);
   return hipGetLastError();
 }
 
 template <int KIND>
 static hipError_t gemm_launch(const PrefillArgs &a, bool shared, int ny, hipStream_t st) {
-  const int tiles = shared ? (a.T + kBM - 1) / kBM : prefill_max_tiles(a.T, a.k, a.E);
+  const int tiles = shared ? (a.T + a.bm - 1) / a.bm : prefill_max_tiles(a.T, a.k, a.E, a.bm);
   const int blocks = (tiles + kXcds - 1) / kXcds * kXcds * ny;
+  if (a.bm != prefill_tile_slots(a.fmt)) return hipErrorInvalidValue;
 #define L(BF) QMOE_LAUNCH((grouped_gemm<KIND, BF>), dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny)
   switch (a.fmt) {
   case kBF16: L(kBF16); break;
@@ -616,11 +601,11 @@ static hipError_t gemm_launch(const PrefillArgs &a, bool shared, int ny, hipStre
 }
 
 hipError_t launch_prefill_gate_up(const PrefillArgs &a, bool shared, hipStream_t st) {
-  return gemm_launch<kGateUp>(a, shared, (shared ? a.Is : a.I) / 64, st);
+  return gemm_launch<kGateUp>(a, shared, (shared ? a.Is : a.I) / (kBN / 2), st);
 }
 
 hipError_t launch_prefill_down(const PrefillArgs &a, bool shared, hipStream_t st) {
-  return gemm_launch<kDown>(a, shared, a.H / 128, st);
+  return gemm_launch<kDown>(a, shared, a.H / kBN, st);
 }
 
 hipError_t launch_prefill_combine(const PrefillArgs &a, float *out, hipStream_t st) {

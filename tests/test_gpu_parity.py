@@ -311,12 +311,12 @@ def check_mfma_layer(cfg, hw, x, scope=None):
 PREFILL = [
     # (router fmt, expert and shared fmt, shared_inter, scope)
     (qmoe.BF16, qmoe.BF16, 0, 0),
-    (qmoe.BF16, qmoe.BF16, 64, 16),
+    (qmoe.BF16, qmoe.BF16, 128, 16),
     (qmoe.F32, qmoe.BF16, 128, 0),
     (qmoe.BF16, qmoe.INT8G32, 0, 0),
-    (qmoe.BF16, qmoe.INT8G32, 64, 16),
+    (qmoe.BF16, qmoe.INT8G32, 128, 16),
     (qmoe.F32, qmoe.INT4G32, 128, 0),
-    (qmoe.BF16, qmoe.INT4G32, 64, 16),
+    (qmoe.BF16, qmoe.INT4G32, 128, 16),
 ]
 
 
@@ -334,8 +334,8 @@ def test_prefill_layers(fmts, T):
 
 
 def test_prefill_skewed_routing():
-    """One expert takes most tokens (several 128-slot tiles), most take none."""
-    cfg = qmoe.LayerConfig(256, 16, 2, 128, 64, 16, qmoe.BF16, qmoe.BF16, qmoe.BF16, "skew")
+    """One expert takes most tokens (several tiles), most take none."""
+    cfg = qmoe.LayerConfig(256, 16, 2, 128, 128, 16, qmoe.BF16, qmoe.BF16, qmoe.BF16, "skew")
     announce("prefill skewed routing T=400")
     hw = qmoe.synthetic_weights(cfg, 41, quantizer=oracle.host_quantizer, router_scale=4.0)
     x = qmoe.synthetic_tokens(cfg, 400, 41)
@@ -343,7 +343,7 @@ def test_prefill_skewed_routing():
     x = (x + 3.0 * r[5] / np.linalg.norm(r[5]) * np.sqrt(256)).astype(np.float32)
     out, ids, _ = check_mfma_layer(cfg, hw, x)
     counts = np.bincount(ids.reshape(-1), minlength=16)
-    assert counts.max() > 256, counts  # the hot expert spans three tiles
+    assert counts.max() > 256, counts  # the hot expert spans several tiles
 
 
 def test_prefill_qwen3_shape_rows_are_independent():
