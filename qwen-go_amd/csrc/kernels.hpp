@@ -116,6 +116,7 @@ struct PrefillPlan {
   float *wslot;                 // (slots) routing weight, or the shared gate
   int32_t *slot_of;             // (T, k) slot of each (token, rank)
   int32_t *grp_off, *grp_cnt;   // (E + 1) first slot and slot count per group
+  int32_t *cursor;              // (E) next free slot per expert while scattering
   int32_t *tile_grp, *tile_m0;  // tile table: group and first row of each tile
   int32_t *n_tiles;             // [0] routed tiles, [1] shared tiles (after the routed ones)
 };
@@ -131,7 +132,7 @@ struct PrefillArgs {
   const uint8_t *sgate, *sup, *sdown;  // shared: (Is, H), (Is, H), down (H, Is)
   const uint16_t *sgate_s, *sup_s, *sdown_s;
   uint16_t *act;                // (slots, Imax) SwiGLU output, bf16
-  float *y;                     // (slots, H) weighted expert outputs
+  uint16_t *y;                  // (slots, H) weighted expert outputs, bf16
 };
 bool prefill_supported(int expert_fmt, int shared_fmt, int H, int I, int Is);
 int prefill_tile_slots(int expert_fmt);              // slots per GEMM tile for the format

@@ -66,7 +66,8 @@ struct qmoe_layer {
   // batched (MFMA) path buffers, present when ws_mfma
   bool ws_mfma = false;
   uint16_t *xb = nullptr, *act = nullptr;
-  float *sg = nullptr, *y = nullptr;
+  float *sg = nullptr;
+  uint16_t *y = nullptr;
   PrefillPlan plan{};
   unsigned int *fallbacks = nullptr;  // tokens routed by the exact fallback
   // decode (T = 1): the expert kernel computes the router partials itself and
@@ -289,7 +290,7 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   const int bm = prefill_tile_slots(d.expert_fmt);
   const size_t tiles = (size_t)prefill_max_tiles(nT, d.top_k, d.n_experts, bm) + (nT + bm - 1) / bm;
   const int imax = std::max(d.moe_inter, d.shared_inter);
-  size_t o_xb = 0, o_sg = 0, o_tok = 0, o_wsl = 0, o_slot = 0, o_goff = 0, o_gcnt = 0, o_tg = 0, o_tm = 0,
+  size_t o_xb = 0, o_sg = 0, o_tok = 0, o_wsl = 0, o_slot = 0, o_goff = 0, o_gcnt = 0, o_cur = 0, o_tg = 0, o_tm = 0,
          o_nt = 0, o_act = 0, o_y = 0;
   if (want_mfma) {
     o_xb = take((size_t)nT * d.hidden * 2);
@@ -299,11 +300,12 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
     o_slot = take(pairs * 4);
     o_goff = take((size_t)(d.n_experts + 1) * 4);
     o_gcnt = take((size_t)(d.n_experts + 1) * 4);
+    o_cur = take((size_t)(d.n_experts + 1) * 4);
     o_tg = take(tiles * 4);
     o_tm = take(tiles * 4);
     o_nt = take(2 * 4);
     o_act = take(slots * imax * 2);
-    o_y = take(slots * d.hidden * 4);
+    o_y = take(slots * d.hidden * 2);
   }
   // Pending work of earlier calls may still read the old workspace.
   if (user_stream) HIP_TRY(l, hipStreamSynchronize(user_stream), "hipStreamSynchronize");
@@ -333,11 +335,12 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
     l->plan.slot_of = (int32_t *)(b + o_slot);
     l->plan.grp_off = (int32_t *)(b + o_goff);
     l->plan.grp_cnt = (int32_t *)(b + o_gcnt);
+    l->plan.cursor = (int32_t *)(b + o_cur);
     l->plan.tile_grp = (int32_t *)(b + o_tg);
     l->plan.tile_m0 = (int32_t *)(b + o_tm);
     l->plan.n_tiles = (int32_t *)(b + o_nt);
     l->act = (uint16_t *)(b + o_act);
-    l->y = (float *)(b + o_y);
+    l->y = (uint16_t *)(b + o_y);
   }
   l->ws_T = nT;
   return QMOE_OK;

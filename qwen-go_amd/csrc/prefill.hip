@@ -9,18 +9,18 @@
 //             range, then a scatter of every pair into its expert's range
 //             (tok[slot], its routing weight, slot_of[t*k + r]).  The shared
 //             expert is group E, owning slots [T*k, T*k + T) in token order.
-//             Also the tile table: one entry per 128 slots of a group.
-//   gate_up   grouped GEMM: per (tile, 64 intermediate columns) a 128 x 128
-//             output block = 128 gathered bf16 rows of x times the expert's
-//             gate rows [n0, n0+64) and up rows [I+n0, I+n0+64) over K = H,
+//             Also the tile table: one entry per BM slots of a group.
+//   gate_up   grouped GEMM: per (tile, 128 intermediate columns) a BM x 256
+//             output block = BM gathered bf16 rows of x times the expert's
+//             gate rows [n0, n0+128) and up rows [I+n0, I+n0+128) over K = H,
 //             on v_mfma_f32_32x32x16_bf16 with f32 accumulation; SwiGLU in the
 //             epilogue (model/moe.go:64-75): act = silu(g) * u, stored bf16.
-//   down      grouped GEMM: act rows of the tile times 128 rows of the
+//   down      grouped GEMM: act rows of the tile times 256 rows of the
 //             expert's down matrix, (H, I) reference layout, over K = I; the
-//             routing weight (or shared gate) scales
-//             the f32 result, y[slot] = w * (down . act) (model/moe.go:76-84).
+//             routing weight (or shared gate) scales the f32 result,
+//             y[slot] = w * (down . act) (model/moe.go:76-84), stored bf16.
 //   combine   out[t] = sum over ranks r in rank order of y[slot_of[t, r]],
-//             then + y[shared slot of t] (model/moe.go:82-97).
+//             then + y[shared slot of t] (model/moe.go:82-97), in f32.
 // The slot order inside an expert comes from LDS atomics and may vary from run
 // to run; every output row depends only on its own token, so results do not.
 //
@@ -89,15 +89,34 @@ __global__ void __launch_bounds__(256) prep_kernel(const float *__restrict__ x, 
 
 constexpr int kDispatchThreads = 1024;
 
+// Counts and slot ranges, one workgroup: J pairs per thread, all loaded up
+// front so that the global loads overlap (0 = a plain loop for any count).
+// Writes each expert's first slot and count, the tile table, and the expert
+// cursors that scatter_kernel advances.
+template <int J>
 __global__ void __launch_bounds__(kDispatchThreads)
-    dispatch_kernel(const int32_t *__restrict__ ids, const float *__restrict__ wts, const float *__restrict__ sg,
-                    int T, int k, int E, int with_shared, int bm, PrefillPlan p) {
-  __shared__ int cnt[1024], incl[1024], tincl[1024], cur[1024];
+    dispatch_kernel(const int32_t *__restrict__ ids, int T, int k, int E, int with_shared, int bm, PrefillPlan p) {
+  __shared__ int cnt[1024], incl[1024], tincl[1024];
   const int tid = threadIdx.x;
   const int n = T * k;
+  constexpr int JJ = J > 0 ? J : 1;
+  int id[JJ];
+  if constexpr (J > 0) {
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int i = tid + j * kDispatchThreads;
+      id[j] = i < n ? ids[i] : -1;
+    }
+  }
   cnt[tid] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += kDispatchThreads) atomicAdd(&cnt[ids[i]], 1);
+  if constexpr (J > 0) {
+#pragma unroll
+    for (int j = 0; j < J; j++)
+      if (id[j] >= 0) atomicAdd(&cnt[id[j]], 1);
+  } else {
+    for (int i = tid; i < n; i += kDispatchThreads) atomicAdd(&cnt[ids[i]], 1);
+  }
   __syncthreads();
   // inclusive scans of the counts and of the tiles per expert (E <= 1024)
   const int c = tid < E ? cnt[tid] : 0;
@@ -118,7 +137,7 @@ __global__ void __launch_bounds__(kDispatchThreads)
   if (tid < E) {
     p.grp_off[tid] = off;
     p.grp_cnt[tid] = c;
-    cur[tid] = off;
+    p.cursor[tid] = off;
     for (int q = 0; q < ct; q++) {
       p.tile_grp[toff + q] = tid;
       p.tile_m0[toff + q] = q * bm;
@@ -135,18 +154,26 @@ __global__ void __launch_bounds__(kDispatchThreads)
     p.grp_off[E] = n;
     p.grp_cnt[E] = with_shared ? T : 0;
   }
-  __syncthreads();
-  for (int i = tid; i < n; i += kDispatchThreads) {
-    const int slot = atomicAdd(&cur[ids[i]], 1);
+}
+
+// Every (token, rank) pair into its expert's slot range -- one pair per
+// thread, spread over the whole device (the stores land anywhere); then the
+// shared expert's slots in token order.
+__global__ void __launch_bounds__(256) scatter_kernel(const int32_t *__restrict__ ids, const float *__restrict__ wts,
+                                                      const float *__restrict__ sg, int T, int k, int with_shared,
+                                                      PrefillPlan p) {
+  const int n = T * k;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    const int slot = atomicAdd(&p.cursor[ids[i]], 1);
     p.tok[slot] = i / k;
     p.wslot[slot] = wts[i];
     p.slot_of[i] = slot;
+  } else if (with_shared && i - n < T) {
+    const int t = i - n;
+    p.tok[n + t] = t;
+    p.wslot[n + t] = sg[t];
   }
-  if (with_shared)
-    for (int t = tid; t < T; t += kDispatchThreads) {
-      p.tok[n + t] = t;
-      p.wslot[n + t] = sg[t];
-    }
 }
 
 // ------------------------------------------------------------ tile setup
@@ -213,7 +240,7 @@ struct GemmCfg {
   static constexpr int kBPieces = kRaw / 16 / kGemmThreads;         // B pieces per thread per step
   static constexpr int kScale = kQuant ? kBPieces * kGemmThreads * 4 : 0;  // a scale dword per code piece
   static constexpr int kBSize = kRaw + kScale;                      // one B ring stage
-  static constexpr int kBStages = kQuant ? (BF == kINT8 ? 2 : 3) : 2;  // B ring: kBStages - 1 steps ahead
+  static constexpr int kBStages = kQuant ? (BF == kINT8 ? 2 : 3) : 3;  // B ring: kBStages - 1 steps ahead
   static constexpr int kTile = kQuant ? kBStage : 16;               // one dequantised B tile
   static constexpr int kBLoads = kQuant ? 2 * kBPieces : kBPieces;  // B loads per thread per step
   static constexpr int kRB = kBM / 4;                               // slots per wave
@@ -519,7 +546,7 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
             const float ws = a.p.wslot[slot];
 #pragma unroll
             for (int q = 0; q < 4; q++)
-              a.y[(size_t)slot * H + n0 + wn * 128 + q * 32 + l32] = ws * acc[b][q][4 * j4 + i];
+              a.y[(size_t)slot * H + n0 + wn * 128 + q * 32 + l32] = f32_to_bf16_rne(ws * acc[b][q][4 * j4 + i]);
           }
         }
   }
@@ -527,26 +554,22 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
 
 // --------------------------------------------------------------- combine
 
-__global__ void __launch_bounds__(256) combine_kernel(const float *__restrict__ y, const int32_t *__restrict__ slot_of,
+__global__ void __launch_bounds__(256) combine_kernel(const uint16_t *__restrict__ y, const int32_t *__restrict__ slot_of,
                                                       int T, int k, int H, int with_shared,
                                                       float *__restrict__ out) {
   const int t = blockIdx.x;
+  auto add4 = [](float4 &acc, uint2 v) {  // four bf16 -> f32, in column order
+    acc.x += bf16_to_f32(v.x & 0xffffu);
+    acc.y += bf16_to_f32(v.x >> 16);
+    acc.z += bf16_to_f32(v.y & 0xffffu);
+    acc.w += bf16_to_f32(v.y >> 16);
+  };
   for (int j = threadIdx.x * 4; j < H; j += 1024) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int r = 0; r < k; r++) {  // rank order, model/moe.go:82-84
-      const float4 v = *reinterpret_cast<const float4 *>(y + (size_t)slot_of[(size_t)t * k + r] * H + j);
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
-    }
-    if (with_shared) {  // added after the routed sum, model/moe.go:94-96
-      const float4 v = *reinterpret_cast<const float4 *>(y + ((size_t)T * k + t) * H + j);
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
-    }
+    for (int r = 0; r < k; r++)  // rank order, model/moe.go:82-84
+      add4(acc, *reinterpret_cast<const uint2 *>(y + (size_t)slot_of[(size_t)t * k + r] * H + j));
+    if (with_shared)  // added after the routed sum, model/moe.go:94-96
+      add4(acc, *reinterpret_cast<const uint2 *>(y + ((size_t)T * k + t) * H + j));
     *reinterpret_cast<float4 *>(out + (size_t)t * H + j) = acc;
   }
 }
@@ -579,8 +602,17 @@ hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, con
   const bool with_shared = a.Is > 0;
   QMOE_LAUNCH(prep_kernel, dim3(a.T), dim3(256), 0, st, x, a.H, with_shared ? shared_gate : nullptr, a.xb,
                      sg);
-  QMOE_LAUNCH(dispatch_kernel, dim3(1), dim3(kDispatchThreads), 0, st, ids, wts, sg, a.T, a.k, a.E,
-                     (int)with_shared, a.bm, a.p);
+  const int n = a.T * a.k;
+#define L(J) QMOE_LAUNCH(dispatch_kernel<J>, dim3(1), dim3(kDispatchThreads), 0, st, ids, a.T, a.k, a.E, \
+                         (int)with_shared, a.bm, a.p)
+  if (n <= 4 * kDispatchThreads) L(4);
+  else if (n <= 16 * kDispatchThreads) L(16);
+  else if (n <= 48 * kDispatchThreads) L(48);
+  else L(0);
+#undef L
+  const int items = n + (with_shared ? a.T : 0);
+  QMOE_LAUNCH(scatter_kernel, dim3((items + 255) / 256), dim3(256), 0, st, ids, wts, sg, a.T, a.k, (int)with_shared,
+              a.p);
   return hipGetLastError();
 }
 
