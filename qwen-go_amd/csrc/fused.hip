@@ -370,6 +370,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
 #pragma unroll
         for (int r = 0; r < BR; r++)  // every pointer first, then every load
           if (r < n) bp[r] = row_ptr(rs_u + r);
+        // row r starts a new set of down scales (run or scale group changes)
+        auto newset = [&](int r) { return r == 0 || bp[r].q != bp[r - 1].q || bp[r].grp != bp[r - 1].grp; };
 #pragma unroll
         for (int r = 0; r < BR; r++) {
           if (r < n) {
@@ -388,11 +390,15 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
               bu[r][c] = load_nt(bp[r].u + off);
             }
             if constexpr (fmt_quant(FMT)) {
-              // the lane's outputs: chunk c covers EPC consecutive outputs
+              // the down scales of the lane's outputs (chunk c covers EPC
+              // consecutive outputs), once per run of rows sharing a run and
+              // a 32-row scale group
+              if (newset(r)) {
 #pragma unroll
-              for (int v = 0; v < SV; v++) {
-                const int c = v / (EPC / 8), part = v % (EPC / 8);
-                bs[r][v] = *reinterpret_cast<const uint4 *>(bp[r].ds + (sl + c * lpr) * EPC + part * 8);
+                for (int v = 0; v < SV; v++) {
+                  const int c = v / (EPC / 8), part = v % (EPC / 8);
+                  bs[r][v] = *reinterpret_cast<const uint4 *>(bp[r].ds + (sl + c * lpr) * EPC + part * 8);
+                }
               }
             }
           }
@@ -425,30 +431,83 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
         for (int c = 0; c < IT; c++)
 #pragma unroll
           for (int e = 0; e < EPC; e++) acc0[c][e] = acc1[c][e] = 0.0f;
+        if constexpr (fmt_quant(FMT) && IT * EPC > 32) {
+          // wide rows (no registers for a set's sum): scale each row's products
+          uint4 sv[SV];
 #pragma unroll
-        for (int r = 0; r < BR; r++) {
-          if (r < n) {
+          for (int v = 0; v < SV; v++) sv[v] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-            for (int c = 0; c < IT; c++) {
-              const uint4 v = *reinterpret_cast<const uint4 *>(wl + (r * IT + c) * 1024 + sl * 16);
-              float w[EPC];
+          for (int r = 0; r < BR; r++) {
+            if (r < n) {
+              if (newset(r)) {
 #pragma unroll
-              for (int e = 0; e < EPC; e++) w[e] = 0.0f;
-              chunk_axpy<FMT>(v, act[r], w);
-              if constexpr (fmt_quant(FMT)) {
+                for (int v = 0; v < SV; v++) sv[v] = bs[r][v];
+              }
+#pragma unroll
+              for (int c = 0; c < IT; c++) {
+                float w[EPC];
+#pragma unroll
+                for (int e = 0; e < EPC; e++) w[e] = 0.0f;
+                chunk_axpy<FMT>(*reinterpret_cast<const uint4 *>(wl + (r * IT + c) * 1024 + sl * 16), act[r], w);
 #pragma unroll
                 for (int e = 0; e < EPC; e++) {
                   const int k = c * EPC + e;  // the lane's k-th output
-                  const uint32_t word = (&bs[r][k / 8].x)[(k % 8) / 2];
-                  w[e] *= f16_to_f32((uint16_t)((k & 1) ? (word >> 16) : (word & 0xffffu)));
+                  const uint32_t word = (&sv[k / 8].x)[(k % 8) / 2];
+                  const float sc = f16_to_f32((uint16_t)((k & 1) ? (word >> 16) : (word & 0xffffu)));
+                  if (bp[r].q == 0) acc0[c][e] = fmaf(w[e], sc, acc0[c][e]);
+                  else acc1[c][e] = fmaf(w[e], sc, acc1[c][e]);
                 }
               }
-              if (bp[r].q == 0) {
+            }
+          }
+        } else if constexpr (fmt_quant(FMT)) {
+          // sum act * code over the rows of one scale set, then scale once
+          float tmp[IT][EPC];
+          uint4 sv[SV];
+          int tq = 0;
 #pragma unroll
-                for (int e = 0; e < EPC; e++) acc0[c][e] += w[e];
-              } else {
+          for (int c = 0; c < IT; c++)
 #pragma unroll
-                for (int e = 0; e < EPC; e++) acc1[c][e] += w[e];
+            for (int e = 0; e < EPC; e++) tmp[c][e] = 0.0f;
+#pragma unroll
+          for (int v = 0; v < SV; v++) sv[v] = make_uint4(0u, 0u, 0u, 0u);
+          auto flush_set = [&]() {
+#pragma unroll
+            for (int c = 0; c < IT; c++)
+#pragma unroll
+              for (int e = 0; e < EPC; e++) {
+                const int k = c * EPC + e;  // the lane's k-th output
+                const uint32_t word = (&sv[k / 8].x)[(k % 8) / 2];
+                const float sc = f16_to_f32((uint16_t)((k & 1) ? (word >> 16) : (word & 0xffffu)));
+                if (tq == 0) acc0[c][e] = fmaf(tmp[c][e], sc, acc0[c][e]);
+                else acc1[c][e] = fmaf(tmp[c][e], sc, acc1[c][e]);
+                tmp[c][e] = 0.0f;
+              }
+          };
+#pragma unroll
+          for (int r = 0; r < BR; r++) {
+            if (r < n) {
+              if (newset(r)) {
+                if (r > 0) flush_set();
+#pragma unroll
+                for (int v = 0; v < SV; v++) sv[v] = bs[r][v];
+                tq = bp[r].q;
+              }
+#pragma unroll
+              for (int c = 0; c < IT; c++)
+                chunk_axpy<FMT>(*reinterpret_cast<const uint4 *>(wl + (r * IT + c) * 1024 + sl * 16), act[r], tmp[c]);
+            }
+          }
+          flush_set();
+        } else {
+#pragma unroll
+          for (int r = 0; r < BR; r++) {
+            if (r < n) {
+#pragma unroll
+              for (int c = 0; c < IT; c++) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(wl + (r * IT + c) * 1024 + sl * 16);
+                if (bp[r].q == 0) chunk_axpy<FMT>(v, act[r], acc0[c]);
+                else chunk_axpy<FMT>(v, act[r], acc1[c]);
               }
             }
           }
