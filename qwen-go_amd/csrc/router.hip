@@ -47,113 +47,157 @@ __global__ void __launch_bounds__(64) router_rowwise_kernel(const float *__restr
   logits[(size_t)t * E + e] = acc;
 }
 
-// Register-tiled SIMT product for many tokens: a 256-thread block computes a
-// 32-token x 32-expert tile, 2 x 2 outputs per thread (tokens ty, ty + 16 and
-// experts tx, tx + 16), staging 32-wide k slices of x and of the router in LDS
-// with k contiguous.  Small tiles keep every SIMD busy: the work is one
-// dependent f32 add chain of length H per output.  Every output still sums its
-// products in h order, so the result equals the row-wise kernel's bit for bit.
+// A raw 16-byte router chunk widened to f32 exactly as router_chunk does.
 template <int FMT>
+__device__ inline void widen_chunk(const uint4 raw, uint16_t scale, float (&wv)[Chunk<FMT>::kElems]) {
+  const uint32_t u[4] = {raw.x, raw.y, raw.z, raw.w};
+  if constexpr (FMT == kF32) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) wv[k] = __uint_as_float(u[k]);
+  } else if constexpr (FMT == kBF16) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      wv[2 * k] = __uint_as_float(u[k] << 16);
+      wv[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+    }
+  } else if constexpr (FMT == kINT8) {
+    const float sc = f16_to_f32(scale);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) wv[4 * k + b] = (float)(int8_t)((u[k] >> (8 * b)) & 0xffu) * sc;
+  } else {
+    const float sc = f16_to_f32(scale);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const uint32_t byte = (u[k] >> (8 * b)) & 0xffu;
+        wv[8 * k + 2 * b] = (float)((int)(byte >> 4) - 8) * sc;
+        wv[8 * k + 2 * b + 1] = (float)((int)(byte & 0xfu) - 8) * sc;
+      }
+  }
+}
+
+// Register-tiled SIMT product for many tokens: a 256-thread block computes a
+// (16 RM)-token x (16 RN)-expert tile, RM x RN outputs per thread (tokens
+// ty + 16 i, experts tx + 16 j), staging KB-wide k slices (KB divides H) of x
+// and of the router in LDS with k contiguous; the next slice is loaded raw into
+// registers while the current one is multiplied.  Every output sums its
+// products in h order, so the result equals the row-wise kernel's bit for bit.
+template <int FMT, int RM, int RN, int KB>
 __global__ void __launch_bounds__(256) router_tiled_kernel(const float *__restrict__ x, int T, int H,
                                                            const uint8_t *__restrict__ w,
                                                            const uint16_t *__restrict__ s, int E,
                                                            float *__restrict__ logits) {
 #pragma clang fp contract(off)
-  constexpr int KB = 32, TM = 32, TN = 32, LD = KB + 4;
+  constexpr int TM = 16 * RM, TN = 16 * RN, LD = KB + 4;
   __shared__ __align__(16) float xs[TM][LD];
   __shared__ __align__(16) float ws[TN][LD];
   const int tid = threadIdx.x;
   const int tx = tid & 15, ty = tid >> 4;
   const int t0 = blockIdx.y * TM, e0 = blockIdx.x * TN;
   constexpr int EPC = Chunk<FMT>::kElems;
-  constexpr int CPR = KB / EPC;  // 16-byte chunks per row per k slice
+  constexpr int CPR = KB / EPC;                        // 16-byte router chunks per row per slice
+  constexpr int NXP = TM * KB / 4, NWP = TN * CPR;     // float4 pieces of x, router chunks per slice
+  constexpr int XPT = (NXP + 255) / 256, WPT = (NWP + 255) / 256;
   const int64_t row_bytes = fmt_matrix_bytes(FMT, 1, H);
   const int nsc = H / kGroup;
 
-  static_assert(TN * CPR <= 256, "one router chunk per thread and slice");
-  // this thread's share of a slice: one float4 of x, at most one 16-byte
-  // router chunk; the next slice is loaded raw into registers while the
-  // current one is multiplied, and widened once it is stored
-  const int xr = tid >> 3, xc4 = tid & 7;
-  const bool x_ok = t0 + xr < T;
-  const float *xsrc = x + (size_t)min(t0 + xr, T - 1) * H + xc4 * 4;
-  const int wr = tid / CPR, wc = tid % CPR;
-  const bool w_ok = tid < TN * CPR && e0 + wr < E;
-  const uint8_t *wrow = w + (size_t)min(e0 + wr, E - 1) * row_bytes;
-  const uint16_t *wsrow = fmt_quant(FMT) ? s + (size_t)min(e0 + wr, E - 1) * nsc : nullptr;
-  float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-  uint4 wraw = make_uint4(0u, 0u, 0u, 0u);
-  uint16_t wsc = 0;
+  // this thread's pieces of a slice: x piece p -> row p / (KB / 4), float4
+  // (p % (KB / 4)); router chunk q -> row q / CPR, chunk q % CPR.  Rows are
+  // clamped in bounds and the loads are unconditional (x_ok / w_ok zero the
+  // stores), so the wait counts of the pipelined loads stay exact.
+  const float *xsrc[XPT];
+  bool x_in[XPT], x_ok[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; i++) {
+    const int p = tid + 256 * i;
+    const int r = min(p / (KB / 4), TM - 1);
+    x_in[i] = p < NXP;
+    x_ok[i] = x_in[i] && t0 + r < T;
+    xsrc[i] = x + (size_t)min(t0 + r, T - 1) * H + (p % (KB / 4)) * 4;
+  }
+  const uint8_t *wrow[WPT];
+  const uint16_t *wsrow[WPT];
+  bool w_in[WPT], w_ok[WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; i++) {
+    const int q = tid + 256 * i;
+    const int r = min(q / CPR, TN - 1);
+    w_in[i] = q < NWP;
+    w_ok[i] = w_in[i] && e0 + r < E;
+    wrow[i] = w + (size_t)min(e0 + r, E - 1) * row_bytes;
+    wsrow[i] = fmt_quant(FMT) ? s + (size_t)min(e0 + r, E - 1) * nsc : nullptr;
+  }
+  float4 xv[XPT];
+  uint4 wraw[WPT];
+  uint16_t wsc[WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; i++) wsc[i] = 0;
   auto load_slice = [&](int k0) {
-    if (x_ok) xv = *reinterpret_cast<const float4 *>(xsrc + k0);
-    if (w_ok) {
-      const int chunk = k0 / EPC + wc;
-      wraw = *reinterpret_cast<const uint4 *>(wrow + (size_t)chunk * 16);
-      if constexpr (fmt_quant(FMT)) wsc = wsrow[(chunk * EPC) / kGroup];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) xv[i] = *reinterpret_cast<const float4 *>(xsrc[i] + k0);
+#pragma unroll
+    for (int i = 0; i < WPT; i++) {
+      const int chunk = k0 / EPC + (tid + 256 * i) % CPR;
+      wraw[i] = *reinterpret_cast<const uint4 *>(wrow[i] + (size_t)chunk * 16);
+      if constexpr (fmt_quant(FMT)) wsc[i] = wsrow[i][(chunk * EPC) / kGroup];
     }
   };
 
-  float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+  float acc[RM][RN];
+#pragma unroll
+  for (int i = 0; i < RM; i++)
+#pragma unroll
+    for (int j = 0; j < RN; j++) acc[i][j] = 0.0f;
   load_slice(0);
   for (int k0 = 0; k0 < H; k0 += KB) {
-    *reinterpret_cast<float4 *>(&xs[xr][xc4 * 4]) = xv;
-    if (tid < TN * CPR) {  // widen the router chunk exactly as router_chunk does
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+      const int p = tid + 256 * i;
+      if (x_in[i])
+        *reinterpret_cast<float4 *>(&xs[p / (KB / 4)][(p % (KB / 4)) * 4]) =
+            x_ok[i] ? xv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < WPT; i++) {
+      if (!w_in[i]) continue;
+      const int q = tid + 256 * i, r = q / CPR, c = q % CPR;
       float wv[EPC];
-      const uint32_t u[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
-      if constexpr (FMT == kF32) {
+      widen_chunk<FMT>(wraw[i], wsc[i], wv);
 #pragma unroll
-        for (int i = 0; i < 4; i++) wv[i] = __uint_as_float(u[i]);
-      } else if constexpr (FMT == kBF16) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          wv[2 * i] = __uint_as_float(u[i] << 16);
-          wv[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-        }
-      } else if constexpr (FMT == kINT8) {
-        const float sc = f16_to_f32(wsc);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int b = 0; b < 4; b++) wv[4 * i + b] = (float)(int8_t)((u[i] >> (8 * b)) & 0xffu) * sc;
-      } else {
-        const float sc = f16_to_f32(wsc);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int b = 0; b < 4; b++) {
-            const uint32_t byte = (u[i] >> (8 * b)) & 0xffu;
-            wv[8 * i + 2 * b] = (float)((int)(byte >> 4) - 8) * sc;
-            wv[8 * i + 2 * b + 1] = (float)((int)(byte & 0xfu) - 8) * sc;
-          }
-      }
-#pragma unroll
-      for (int q = 0; q < EPC; q++) ws[wr][wc * EPC + q] = w_ok ? wv[q] : 0.0f;
+      for (int q2 = 0; q2 < EPC; q2 += 4)
+        *reinterpret_cast<float4 *>(&ws[r][c * EPC + q2]) =
+            w_ok[i] ? make_float4(wv[q2], wv[q2 + 1], wv[q2 + 2], wv[q2 + 3]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
-    if (k0 + KB < H) load_slice(k0 + KB);
+    load_slice(min(k0 + KB, H - KB));
 #pragma unroll
     for (int kk = 0; kk < KB; kk += 4) {
-      const float4 a0 = *reinterpret_cast<const float4 *>(&xs[ty][kk]);
-      const float4 a1 = *reinterpret_cast<const float4 *>(&xs[ty + 16][kk]);
-      const float4 b0 = *reinterpret_cast<const float4 *>(&ws[tx][kk]);
-      const float4 b1 = *reinterpret_cast<const float4 *>(&ws[tx + 16][kk]);
-      const float av[2][4] = {{a0.x, a0.y, a0.z, a0.w}, {a1.x, a1.y, a1.z, a1.w}};
-      const float bv[2][4] = {{b0.x, b0.y, b0.z, b0.w}, {b1.x, b1.y, b1.z, b1.w}};
+      float4 av[RM], bv[RN];
 #pragma unroll
-      for (int q = 0; q < 4; q++)
+      for (int i = 0; i < RM; i++) av[i] = *reinterpret_cast<const float4 *>(&xs[ty + 16 * i][kk]);
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+      for (int j = 0; j < RN; j++) bv[j] = *reinterpret_cast<const float4 *>(&ws[tx + 16 * j][kk]);
 #pragma unroll
-          for (int j = 0; j < 2; j++) acc[i][j] = acc[i][j] + av[i][q] * bv[j][q];
+      for (int i = 0; i < RM; i++)
+#pragma unroll
+        for (int j = 0; j < RN; j++) {
+          acc[i][j] = acc[i][j] + av[i].x * bv[j].x;
+          acc[i][j] = acc[i][j] + av[i].y * bv[j].y;
+          acc[i][j] = acc[i][j] + av[i].z * bv[j].z;
+          acc[i][j] = acc[i][j] + av[i].w * bv[j].w;
+        }
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < RM; i++) {
     const int t = t0 + ty + 16 * i;
     if (t >= T) continue;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < RN; j++) {
       const int e = e0 + tx + 16 * j;
       if (e < E) logits[(size_t)t * E + e] = acc[i][j];
     }
@@ -169,9 +213,21 @@ static hipError_t router_logits_fmt(const float *x, int T, const DevMat &r, floa
     QMOE_LAUNCH(router_rowwise_kernel<FMT>, grid, dim3(64), (size_t)H * sizeof(float), st, x,
                        T, H, r.w, r.s, E, logits);
   } else {
-    dim3 grid((E + 31) / 32, (T + 31) / 32);
-    QMOE_LAUNCH(router_tiled_kernel<FMT>, grid, dim3(256), 0, st, x, T, H, r.w, r.s, E,
-                       logits);
+    // 2x2 outputs per lane while that still fills 256 CUs four waves deep,
+    // else one output per lane and four times the workgroups
+    const bool wide = (int64_t)T * E >= (int64_t)4 * 256 * 256;
+    const dim3 b(256), g11((E + 15) / 16, (T + 15) / 16), g22((E + 31) / 32, (T + 31) / 32);
+    if (H % 64 == 0) {
+      if (wide)
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 2, 2, 64>), g22, b, 0, st, x, T, H, r.w, r.s, E, logits);
+      else
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 1, 64>), g11, b, 0, st, x, T, H, r.w, r.s, E, logits);
+    } else {
+      if (wide)
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 2, 2, 32>), g22, b, 0, st, x, T, H, r.w, r.s, E, logits);
+      else
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 1, 32>), g11, b, 0, st, x, T, H, r.w, r.s, E, logits);
+    }
   }
   return hipGetLastError();
 }
@@ -185,8 +241,6 @@ hipError_t launch_router_logits(const float *x, int T, const DevMat &router, flo
   default: return router_logits_fmt<kINT4>(x, T, router, logits, st);
   }
 }
-
-// One wavefront per token: exact softmax + selection + renormalisation on
 
 // One wavefront per token: exact softmax + selection + renormalisation on
 // the exact logits (select.hpp).

@@ -229,6 +229,19 @@ def test_decode_router_exchange_many_calls(fmts):
     assert err <= TOL_F32, f"normwise relative error {err:.3e} > {TOL_F32}"
 
 
+@pytest.mark.parametrize("rf,H,T", [(qmoe.F32, 288, 40), (qmoe.INT8G32, 288, 40), (qmoe.INT4G32, 288, 2100),
+                                     (qmoe.BF16, 320, 2100), (qmoe.BF16, 288, 2100)])
+def test_router_tile_shapes(rf, H, T):
+    """The exact router for T > 32 in each of its tilings: one output per lane
+    (T=40) and four (T=2100 x 128 experts), with 64-wide k slices (H=320) and
+    32-wide ones (H=288).  ids must equal the reference's exactly."""
+    cfg = qmoe.LayerConfig(H, 128, 8, 64, 0, 128, rf, qmoe.BF16, qmoe.BF16, "router-tiles")
+    announce(f"router tiles fmt={rf} H={H} T={T}")
+    hw = qmoe.synthetic_weights(cfg, 7 + T, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, T, 7 + T)
+    check_layer(cfg, hw, x)
+
+
 @pytest.mark.parametrize("T", [1, 5, 40])
 def test_router_exact_ties(T):
     """Identical router rows give exactly equal logits; the reference breaks the
