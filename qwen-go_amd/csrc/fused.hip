@@ -362,8 +362,16 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
         // once the down rows have been consumed.  One lane group = one wave, so
         // rows and experts are wave-uniform and the row bases scalar.
         unsigned char *wl = burst_lds + (size_t)(dt >> 6) * kBurstKB * 1024;
+        // Nothing of this wave is in flight here.  Saying so with a real
+        // s_waitcnt vmcnt(0) (the builtin, which the compiler's wait
+        // insertion sees, unlike asm) clears the loads it believes pending
+        // from other paths into registers this code reuses; otherwise it
+        // waits for a count before each row's loads, which here means
+        // waiting for the first rows' data before issuing the fourth.
+        __builtin_amdgcn_s_waitcnt(0x0f70);
         constexpr int SV = fmt_quant(FMT) ? IT * EPC / 8 : 1;  // 16-byte pieces of a lane's fp16 down scales
         uint4 bg[BR][IT], bu[BR][IT], bs[BR][SV];
+        uint32_t bgs[BR][IT], bus[BR][IT];  // group-32 formats: the gate/up scales of the lane's chunks
         RowPtr bp[BR];
         const int n = __builtin_amdgcn_readfirstlane(re - rs);
         const int rs_u = __builtin_amdgcn_readfirstlane(rs);
@@ -390,6 +398,16 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
               bu[r][c] = load_nt(bp[r].u + off);
             }
             if constexpr (fmt_quant(FMT)) {
+              // loaded with the rows: past wait_x (an atomic spin) the
+              // compiler would issue them only where they are used; the
+              // empty asm after wait_x keeps their conversion (and its
+              // wait) from being hoisted between the rows' loads
+#pragma unroll
+              for (int c = 0; c < IT; c++) {
+                const int ch = sl + c * lpr;
+                bgs[r][c] = bp[r].gs[(ch * EPC) / kGroup];
+                bus[r][c] = bp[r].us[(ch * EPC) / kGroup];
+              }
               // the down scales of the lane's outputs (chunk c covers EPC
               // consecutive outputs), once per run of rows sharing a run and
               // a 32-row scale group
@@ -404,6 +422,12 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
           }
         }
         wait_x();
+        if constexpr (fmt_quant(FMT)) {
+#pragma unroll
+          for (int r = 0; r < BR; r++)
+#pragma unroll
+            for (int c = 0; c < IT; c++) asm volatile("" : "+v"(bgs[r][c]), "+v"(bus[r][c]));
+        }
         float act[BR];
 #pragma unroll
         for (int r = 0; r < BR; r++) {
@@ -416,8 +440,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
               float dg = chunk_dot<FMT>(bg[r][c], xs + ch * EPC);
               float du = chunk_dot<FMT>(bu[r][c], xs + ch * EPC);
               if constexpr (fmt_quant(FMT)) {
-                dg *= f16_to_f32(bp[r].gs[(ch * EPC) / kGroup]);
-                du *= f16_to_f32(bp[r].us[(ch * EPC) / kGroup]);
+                dg *= f16_to_f32((uint16_t)bgs[r][c]);
+                du *= f16_to_f32((uint16_t)bus[r][c]);
               }
               gv += dg;
               uv += du;

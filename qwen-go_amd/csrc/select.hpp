@@ -126,7 +126,12 @@ __device__ __forceinline__ void select_exact_nj(const float *__restrict__ lt, in
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
     const int n = min(64, E - 64 * j);
-    for (int l = 0; l < n; l++) sum = sum + __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v[j]), l));
+    if (n == 64) {  // a full column: constant lane indices, no loop overhead
+#pragma unroll
+      for (int l = 0; l < 64; l++) sum = sum + __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v[j]), l));
+    } else {
+      for (int l = 0; l < n; l++) sum = sum + __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v[j]), l));
+    }
   }
   uint64_t key[NJ];
 #pragma unroll
@@ -206,8 +211,8 @@ __device__ __forceinline__ double wave_max_f64(double v) { return dkey_inv(wave_
 // the reference's logit L_e lies in [S_e - B_e, S_e + B_e].
 //
 // Rounds pick the candidate with the largest S rounded to f32 (each lane
-// caches its own best; a round is one f32 wavefront max plus a ballot for the
-// lowest winning lane).  The order is then certified with the full bounds:
+// sorts its own candidates once, so a round is one f32 wavefront max, a ballot
+// for the lowest winning lane and a shift of the winner's list).  The order is then certified with the full bounds:
 // rank r must beat every candidate still remaining after it -- the later
 // selected ones and all unselected ones -- lower bound over upper bound by
 // delta, enough that p = fl(fl(exp(fl(L - max))) / sum) (tensors.go:106-121)
@@ -237,34 +242,45 @@ __device__ __forceinline__ bool certified_select_regs(const double (&S)[NJ], con
   // upper bound of the reference's max logit (f32 rounding covered by 2^-20)
   const double mh_all = (double)wave_max_f32(mh);
   const double mx_hi = mh_all + fabs(mh_all) * 0x1p-20 + 0x1p-60;
-  int lj = -1;
-  float lbest = -INFINITY;
+  // this lane's candidates sorted by key, descending, equal keys by lower
+  // slot (the one a scan of the slots meets first): a bitonic network over
+  // (key, slot), slot NJ marking an exhausted list
+  static_assert((NJ & (NJ - 1)) == 0, "NJ is a power of two");
+  float hk[NJ];
+  int hj[NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; j++)
-    if (key[j] > lbest || (lj < 0 && key[j] != -INFINITY)) {
-      lbest = key[j];
-      lj = j;
-    }
+  for (int j = 0; j < NJ; j++) {
+    hk[j] = key[j];
+    hj[j] = j;
+  }
+#pragma unroll
+  for (int size = 2; size <= NJ; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+      for (int i = 0; i < NJ; i++) {
+        const int l = i ^ stride;
+        if (l > i) {
+          const bool l_first = hk[l] > hk[i] || (hk[l] == hk[i] && hj[l] < hj[i]);
+          const bool swap = (i & size) == 0 ? l_first : !l_first;
+          const float tk = hk[i];
+          const int tj = hj[i];
+          hk[i] = swap ? hk[l] : hk[i];
+          hj[i] = swap ? hj[l] : hj[i];
+          hk[l] = swap ? tk : hk[l];
+          hj[l] = swap ? tj : hj[l];
+        }
+      }
   int seli = 0;
   double myS = 0.0, myB = 0.0;
   for (int r = 0; r < k; r++) {
-    const float m = wave_max_f32(lbest);
-    const uint64_t win = __ballot(lj >= 0 && lbest == m);
+    const float m = wave_max_f32(hk[0]);
+    const uint64_t win = __ballot(hk[0] != -INFINITY && hk[0] == m);
     const int wl = win ? __ffsll((unsigned long long)win) - 1 : 0;
-    int c = 0;
-    double sc = 0.0, bc = 0.0;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-      const bool mine = j == lj;
-      if (mine) {
-        c = lane + 64 * j;
-        sc = S[j];
-        bc = B[j];
-      }
-    }
-    c = __builtin_amdgcn_readlane(c, wl);
-    sc = readlane_f64(sc, wl);
-    bc = readlane_f64(bc, wl);
+    const int jw = __builtin_amdgcn_readlane(hj[0], wl);  // the winner's slot (uniform)
+    const int c = wl + 64 * jw;
+    // jw is uniform: an indexed register read, not a select over the slots
+    const double sc = readlane_f64(S[jw], wl), bc = readlane_f64(B[jw], wl);
     if (lane == r) {
       seli = c;
       myS = sc;
@@ -276,18 +292,15 @@ __device__ __forceinline__ bool certified_select_regs(const double (&S)[NJ], con
       else if (r == spec_rank)
         __hip_atomic_store(spec_slot, c + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    if (lane == wl) {  // the winner's lane drops it and refreshes its best
+    if (lane == wl) {  // the winner's lane retires the slot and drops its head
+      key[jw] = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < NJ; j++)
-        if (j == lj) key[j] = -INFINITY;
-      lj = -1;
-      lbest = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < NJ; j++)
-        if (key[j] > lbest || (lj < 0 && key[j] != -INFINITY)) {
-          lbest = key[j];
-          lj = j;
-        }
+      for (int j = 0; j + 1 < NJ; j++) {
+        hk[j] = hk[j + 1];
+        hj[j] = hj[j + 1];
+      }
+      hk[NJ - 1] = -INFINITY;
+      hj[NJ - 1] = NJ;
     }
   }
   // largest upper bound among the candidates never selected
