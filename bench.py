@@ -366,9 +366,11 @@ def main():
         },
     }
     fb = sum(L.router_fallbacks() for L in layers)
+    rescued = sum(L.router_rescues() for L in layers)
     result["layer_roofline"]["router_fallbacks"] = {
-        "tokens": int(fb), "of_tokens": int(T * (n_x + args.warmup + args.steps)),
-        "note": "tokens the certified decode router could not certify (recomputed exactly)"}
+        "tokens": int(fb), "rescued": int(rescued), "of_tokens": int(T * (n_x + args.warmup + args.steps)),
+        "note": "tokens the certified decode router could not certify: rescued = settled by exact logits of "
+                "the candidates in doubt; tokens = routed by the full exact path"}
     if skew:
         result["config"]["skew"] = {"target_max_over_median": skew["target_max_over_median"],
                                     "c": skew["per_x"][0]["c"], "max_load": skew["per_x"][0]["max_load"],

@@ -172,6 +172,12 @@ qmoe_status qmoe_profile_read(qmoe_layer *layer, double *stage_ms, int64_t *stag
  * with the exact sequential path.  Synchronises the device. */
 qmoe_status qmoe_router_fallbacks(qmoe_layer *layer, int64_t *count);
 
+/* Diagnostics with no reference counterpart: the number of tokens, since
+ * qmoe_create, whose certification failed at first and succeeded once the
+ * few candidates in doubt had their exact sequential logits computed (no
+ * full exact routing needed).  Synchronises the device. */
+qmoe_status qmoe_router_rescues(qmoe_layer *layer, int64_t *count);
+
 /* Bytes of device memory held by the handle (weights + workspace). */
 int64_t qmoe_device_bytes(const qmoe_layer *layer);
 

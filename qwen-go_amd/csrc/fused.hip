@@ -156,6 +156,7 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   __shared__ int s_ids[64];
   __shared__ float s_w[64];
   __shared__ int s_spec[64];  // tentative expert + 1 per rank, 0 = not yet
+  __shared__ int s_list[64];  // candidates of a certification rescue
   __shared__ float s_sg;
   __shared__ int s_exact;
   __shared__ int s_xready;  // data waves whose share of x is in LDS
@@ -652,13 +653,16 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   if (ctl) {
     // ---- control wave: routing; the shared gate for a shared run
     const bool has_routed = rank0 != a.k;
+    double S[NJ], B[NJ], kth_lo = 0.0;
+    bool rescue = false;  // certification failed: try exact logits of the candidates in doubt
+    int32_t *gi = nullptr;
+    float *gw = nullptr;
     if (a.fused_router) {
       if (has_routed) {
-        double S[NJ], B[NJ];
+        gi = writer ? a.ids : nullptr;
+        gw = writer ? a.weights : nullptr;
         if (poll_router_words<NJ>(a.rtag, a.E, a.epoch, S, B)) {
-          const bool ok = certified_select_regs<NJ>(S, B, a.E, a.k, a.scope, writer ? a.ids : nullptr,
-                                                    writer ? a.weights : nullptr, s_ids, s_w, -2, s_spec);
-          need_exact = !ok;
+          rescue = !certified_select_regs<NJ>(S, B, a.E, a.k, a.scope, gi, gw, s_ids, s_w, -2, s_spec, &kth_lo);
         } else {
           // timed out: flag it for the host (the call's result is not
           // trustworthy), stream expert 0 tentatively and route this
@@ -670,12 +674,32 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
         }
       }
     } else if (has_routed && a.sb) {
-      const bool ok = certified_select_nj<NJ>(a.sb + (size_t)t * a.E * 2, a.E, a.k, a.scope,
-                                              writer ? a.ids + (size_t)t * a.k : nullptr,
-                                              writer ? a.weights + (size_t)t * a.k : nullptr, s_ids, s_w, -2,
-                                              s_spec);
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int e = threadIdx.x + 64 * j;
+        const double2 v =
+            e < a.E ? reinterpret_cast<const double2 *>(a.sb + (size_t)t * a.E * 2)[e] : make_double2(-INFINITY, 0.0);
+        S[j] = v.x;
+        B[j] = v.y;
+      }
+      gi = writer ? a.ids + (size_t)t * a.k : nullptr;
+      gw = writer ? a.weights + (size_t)t * a.k : nullptr;
+      rescue = !certified_select_regs<NJ>(S, B, a.E, a.k, a.scope, gi, gw, s_ids, s_w, -2, s_spec, &kth_lo);
+    }
+    if (rescue) {
+      // a bf16 router (the in-kernel router is one): exact logits of the few
+      // candidates in doubt, while the data waves stream the tentative
+      // experts; other formats, or a failed rescue: the exact path
+      bool ok = false;
+      if (a.rfmt == kBF16) {
+        wait_x();
+        ok = refine_select<kBF16, NJ>(S, B, kth_lo, a.E, a.k, a.scope, xs, H, a.rw, nullptr, s_list, gi, gw, s_ids,
+                                      s_w);
+        if (ok && writer && threadIdx.x == 0) atomicAdd(a.fallbacks + 1, 1u);
+      }
       need_exact = !ok;
-    } else if (has_routed && threadIdx.x < a.k) {  // precomputed routing
+    }
+    if (!a.fused_router && !a.sb && has_routed && threadIdx.x < a.k) {  // precomputed routing
       const int id = a.ids[(size_t)t * a.k + threadIdx.x];
       s_ids[threadIdx.x] = id;
       s_w[threadIdx.x] = a.weights[(size_t)t * a.k + threadIdx.x];

@@ -69,7 +69,7 @@ struct qmoe_layer {
   float *sg = nullptr;
   uint16_t *y = nullptr;
   PrefillPlan plan{};
-  unsigned int *fallbacks = nullptr;  // tokens routed by the exact fallback
+  unsigned int *fallbacks = nullptr;  // [0] tokens routed by the exact fallback, [1] certification rescues
   // decode (T = 1): the expert kernel computes the router partials itself and
   // exchanges them between its workgroups as tagged words (2 per expert)
   uint64_t *rtag = nullptr;
@@ -828,6 +828,18 @@ qmoe_status qmoe_router_fallbacks(qmoe_layer *l, int64_t *count) {
   HIP_TRY(l, hipDeviceSynchronize(), "hipDeviceSynchronize");
   unsigned int v = 0;
   HIP_TRY(l, hipMemcpy(&v, l->fallbacks, sizeof(v), hipMemcpyDeviceToHost), "fallback counter read");
+  *count = v;
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_router_rescues(qmoe_layer *l, int64_t *count) {
+  if (!l || !count) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  HIP_TRY(l, hipDeviceSynchronize(), "hipDeviceSynchronize");
+  unsigned int v = 0;
+  HIP_TRY(l, hipMemcpy(&v, l->fallbacks + 1, sizeof(v), hipMemcpyDeviceToHost), "rescue counter read");
   *count = v;
   return QMOE_OK;
 }

@@ -47,38 +47,6 @@ __global__ void __launch_bounds__(64) router_rowwise_kernel(const float *__restr
   logits[(size_t)t * E + e] = acc;
 }
 
-// A raw 16-byte router chunk widened to f32 exactly as router_chunk does.
-template <int FMT>
-__device__ inline void widen_chunk(const uint4 raw, uint16_t scale, float (&wv)[Chunk<FMT>::kElems]) {
-  const uint32_t u[4] = {raw.x, raw.y, raw.z, raw.w};
-  if constexpr (FMT == kF32) {
-#pragma unroll
-    for (int k = 0; k < 4; k++) wv[k] = __uint_as_float(u[k]);
-  } else if constexpr (FMT == kBF16) {
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      wv[2 * k] = __uint_as_float(u[k] << 16);
-      wv[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
-    }
-  } else if constexpr (FMT == kINT8) {
-    const float sc = f16_to_f32(scale);
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-      for (int b = 0; b < 4; b++) wv[4 * k + b] = (float)(int8_t)((u[k] >> (8 * b)) & 0xffu) * sc;
-  } else {
-    const float sc = f16_to_f32(scale);
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-      for (int b = 0; b < 4; b++) {
-        const uint32_t byte = (u[k] >> (8 * b)) & 0xffu;
-        wv[8 * k + 2 * b] = (float)((int)(byte >> 4) - 8) * sc;
-        wv[8 * k + 2 * b + 1] = (float)((int)(byte & 0xfu) - 8) * sc;
-      }
-  }
-}
-
 // Register-tiled SIMT product for many tokens: a 256-thread block computes a
 // (16 RM)-token x (16 RN)-expert tile, RM x RN outputs per thread (tokens
 // ty + 16 i, experts tx + 16 j), staging KB-wide k slices (KB divides H) of x
@@ -340,13 +308,40 @@ __global__ void __launch_bounds__(256) select_cert_kernel(const float *__restric
                                                           unsigned int *__restrict__ fallbacks) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int ok;
+  __shared__ int s_list[64];
   const int t = blockIdx.x;
   const int E = router.rows, H = router.cols;
   float *xs = reinterpret_cast<float *>(smem);
   float *lt = xs + H;
   if (threadIdx.x < 64) {
-    const bool c = certified_select_nj<NJ>(sb + (size_t)t * E * 2, E, k, scope, ids + (size_t)t * k,
-                                           weights + (size_t)t * k, nullptr, nullptr);
+    const int lane = threadIdx.x;
+    double S[NJ], B[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const int e = lane + 64 * j;
+      const double2 v = e < E ? reinterpret_cast<const double2 *>(sb + (size_t)t * E * 2)[e] : make_double2(-INFINITY, 0.0);
+      S[j] = v.x;
+      B[j] = v.y;
+    }
+    double kth_lo = 0.0;
+    bool c = certified_select_regs<NJ>(S, B, E, k, scope, ids + (size_t)t * k, weights + (size_t)t * k, nullptr,
+                                       nullptr, -1, nullptr, &kth_lo);
+    if (!c) {
+      // exact logits for the few candidates in doubt first
+      for (int i = lane; i < H; i += 64) xs[i] = x[(size_t)t * H + i];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+#define R(F)                                                                                                     \
+  c = refine_select<F, NJ>(S, B, kth_lo, E, k, scope, xs, H, router.w, router.s, s_list, ids + (size_t)t * k, \
+                           weights + (size_t)t * k, nullptr, nullptr)
+      switch (router.fmt) {
+      case kF32: R(kF32); break;
+      case kBF16: R(kBF16); break;
+      case kINT8: R(kINT8); break;
+      default: R(kINT4); break;
+      }
+#undef R
+      if (c && lane == 0) atomicAdd(fallbacks + 1, 1u);
+    }
     if (threadIdx.x == 0) ok = c;
   }
   __syncthreads();

@@ -103,4 +103,107 @@ __device__ __forceinline__ void tagged_sb(double S, double B, uint32_t tag, uint
   wb = tag_word((B + fabs(S) * 0x1p-42) * (1.0 + 0x1p-40), tag);
 }
 
+// A raw 16-byte router chunk widened to f32 exactly as router_chunk does.
+template <int FMT>
+__device__ inline void widen_chunk(const uint4 raw, uint16_t scale, float (&wv)[Chunk<FMT>::kElems]) {
+  const uint32_t u[4] = {raw.x, raw.y, raw.z, raw.w};
+  if constexpr (FMT == kF32) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) wv[k] = __uint_as_float(u[k]);
+  } else if constexpr (FMT == kBF16) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      wv[2 * k] = __uint_as_float(u[k] << 16);
+      wv[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+    }
+  } else if constexpr (FMT == kINT8) {
+    const float sc = f16_to_f32(scale);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) wv[4 * k + b] = (float)(int8_t)((u[k] >> (8 * b)) & 0xffu) * sc;
+  } else {
+    const float sc = f16_to_f32(scale);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const uint32_t byte = (u[k] >> (8 * b)) & 0xffu;
+        wv[8 * k + 2 * b] = (float)((int)(byte >> 4) - 8) * sc;
+        wv[8 * k + 2 * b + 1] = (float)((int)(byte & 0xfu) - 8) * sc;
+      }
+  }
+}
+
+// Rescue of a failed certification (one full wavefront): the candidates
+// whose upper bound reaches the k-th selected one's lower bound (less the f32
+// rounding of the round keys) -- the only ones that can be in the top k or
+// change its order -- get their reference logits computed exactly, one
+// candidate per lane (the sequential f32 sum of model/tensors.go:77-89,
+// model/moe.go:159-162 on x in LDS), and the selection is certified again with
+// their bounds at zero.  S and B are updated in place.  Returns false (nothing
+// written) when more than 64 candidates qualify or certification still fails,
+// which takes a near or exact tie of reference logits.  list: 64 ints of LDS.
+template <int FMT, int NJ>
+__device__ bool refine_select(double (&S)[NJ], double (&B)[NJ], double kth_lo, int E, int k, int scope,
+                              const float *__restrict__ xs, int H, const uint8_t *__restrict__ rw,
+                              const uint16_t *__restrict__ rs, int *list, int32_t *g_ids, float *g_w, int *s_ids,
+                              float *s_w) {
+#pragma clang fp contract(off)
+  constexpr int EPC = Chunk<FMT>::kElems;
+  const int lane = threadIdx.x & 63;
+  const double thr = kth_lo - fabs(kth_lo) * 0x1p-20 - 0x1p-60;
+  bool in[NJ];
+  int idx[NJ];
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const int e = lane + 64 * j;
+    in[j] = e < scope && e < E && S[j] + B[j] >= thr;
+    const uint64_t m = __ballot(in[j]);
+    idx[j] = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    n += __popcll(m);
+  }
+  if (n > 64) return false;
+#pragma unroll
+  for (int j = 0; j < NJ; j++)
+    if (in[j]) list[idx[j]] = lane + 64 * j;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  float L = 0.0f;
+  if (lane < n) {
+    const int e = list[lane];
+    const uint8_t *row = rw + (size_t)e * fmt_matrix_bytes(FMT, 1, H);
+    const uint16_t *srow = fmt_quant(FMT) ? rs + (size_t)e * (H / kGroup) : nullptr;
+    const int nch = H / EPC;
+    for (int c0 = 0; c0 < nch; c0 += 8) {  // eight raw 16-byte chunks in flight, widened one at a time
+      uint4 raw[8];
+      uint16_t sc[8];
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        const int ch = min(c0 + c, nch - 1);
+        raw[c] = *reinterpret_cast<const uint4 *>(row + (size_t)ch * 16);
+        sc[c] = fmt_quant(FMT) ? srow[(ch * EPC) / kGroup] : (uint16_t)0;
+      }
+#pragma unroll
+      for (int c = 0; c < 8; c++)
+        if (c0 + c < nch) {
+          float wv[EPC];
+          widen_chunk<FMT>(raw[c], sc[c], wv);
+#pragma unroll
+          for (int i = 0; i < EPC; i++) L = L + xs[(c0 + c) * EPC + i] * wv[i];
+        }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const float Lj = __uint_as_float(__builtin_amdgcn_ds_bpermute(4 * (idx[j] & 63), __float_as_uint(L)));
+    if (in[j]) {
+      S[j] = (double)Lj;
+      B[j] = 0.0;
+    }
+  }
+  return certified_select_regs<NJ>(S, B, E, k, scope, g_ids, g_w, s_ids, s_w);
+}
+
 }  // namespace qmoe

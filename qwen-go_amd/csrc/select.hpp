@@ -228,7 +228,8 @@ __device__ __forceinline__ double wave_max_f64(double v) { return dkey_inv(wave_
 template <int NJ>
 __device__ __forceinline__ bool certified_select_regs(const double (&S)[NJ], const double (&B)[NJ], int E, int k,
                                                       int scope, int32_t *g_ids, float *g_w, int *s_ids,
-                                                      float *s_w, int spec_rank = -1, int *spec_slot = nullptr) {
+                                                      float *s_w, int spec_rank = -1, int *spec_slot = nullptr,
+                                                      double *kth_lo = nullptr) {
   // spec_rank == -2: publish every rank's tentative expert to spec_slot[rank]
   const int lane = threadIdx.x & 63;
   float key[NJ];
@@ -321,7 +322,11 @@ __device__ __forceinline__ bool certified_select_regs(const double (&S)[NJ], con
     if (rival && !(lo - umax > f32_4ulps(X) + 0x1p-20)) ok = false;
     umax = fmax(umax, s_r + b_r);
   }
-  if (!ok) return false;
+  if (!ok) {
+    // for a rescue: the lower bound of the k-th selected candidate
+    if (kth_lo) *kth_lo = readlane_f64(myS, k - 1) - readlane_f64(myB, k - 1);
+    return false;
+  }
   const double smax = mx_hi;  // >= every logit: exp never overflows
   double z = 0.0;
 #pragma unroll

@@ -70,6 +70,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_profile_enable": ([vp, ctypes.c_uint32], i32),
         "qmoe_profile_read": ([vp, vp, vp, i32], i32),
         "qmoe_router_fallbacks": ([vp, vp], i32),
+        "qmoe_router_rescues": ([vp, vp], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -83,7 +84,8 @@ def exported_symbols() -> list[str]:
     return ["qmoe_create", "qmoe_destroy", "qmoe_last_error", "qmoe_status_string",
             "qmoe_set_router", "qmoe_set_experts", "qmoe_set_shared", "qmoe_quantize_experts",
             "qmoe_quantize_device", "qmoe_forward", "qmoe_forward_device", "qmoe_dequant_debug",
-            "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks"]
+            "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks",
+            "qmoe_router_rescues"]
 
 
 (STAGE_ROUTER, STAGE_SELECT, STAGE_GATE_UP, STAGE_SHARED_GATE_UP, STAGE_DOWN, STAGE_FUSED, STAGE_DISPATCH,
@@ -228,6 +230,13 @@ class MoeLayer:
     def router_fallbacks(self) -> int:
         n = ctypes.c_int64()
         self._check(self.lib.qmoe_router_fallbacks(self.h, ctypes.byref(n)))
+        return int(n.value)
+
+    def router_rescues(self) -> int:
+        """Tokens whose first certification failed and was rescued by exact
+        logits of the candidates in doubt (no full exact routing)."""
+        n = ctypes.c_int64()
+        self._check(self.lib.qmoe_router_rescues(self.h, ctypes.byref(n)))
         return int(n.value)
 
     def device_bytes(self) -> int:

@@ -242,6 +242,41 @@ def test_router_tile_shapes(rf, H, T):
     check_layer(cfg, hw, x)
 
 
+@pytest.mark.parametrize("T", [1, 5, 12])
+def test_router_near_tie_rescue(T):
+    """Two router rows one bf16 ulp apart at their largest weight, where x is
+    +-1: their logits differ by ~1e-4, inside the certified bound at H=2048
+    (~2e-3) but far above the tie margin.  The first certification fails; exact logits of the
+    candidates in doubt settle it without the full exact path, and the order
+    must be the reference's."""
+    cfg = qmoe.LayerConfig(2048, 128, 8, 64, 0, 128, qmoe.BF16, qmoe.BF16, qmoe.BF16, "near-tie")
+    announce(f"router near-tie rescue T={T}")
+    hw = qmoe.synthetic_weights(cfg, 77, quantizer=oracle.host_quantizer)
+    r = hw.router.copy()
+    h0 = int(np.argmax(np.abs(qmoe.bf16_bits_to_f32(r[3]))))  # the largest weight: the widest ulp
+    r[5] = r[3]
+    r[5, h0] = r[3, h0] + 1  # one ulp further from zero
+    hw.router = r
+    x = qmoe.synthetic_tokens(cfg, T, 77)
+    w3 = qmoe.bf16_bits_to_f32(r[3]).astype(np.float32)
+    w2 = qmoe.bf16_bits_to_f32(r[2]).astype(np.float32)
+    x = (x + 40.0 * w3 + 38.0 * w2).astype(np.float32)
+    x[:, h0] = np.sign(w3[h0]) or 1.0
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(x)
+        fb, rescued = layer.router_fallbacks(), layer.router_rescues()
+    finally:
+        layer.close()
+    ref, rids, rw = oracle.OracleLayer(hw).forward(x)
+    assert np.array_equal(ids, rids), (ids, rids)
+    assert set(ids[0][:2]) == {3, 5}, ids[0]
+    np.testing.assert_allclose(w, rw, rtol=1e-4, atol=0)
+    assert rel_err(out, ref) <= TOL_F32
+    assert rescued == T and fb == 0, (rescued, fb)
+
+
 @pytest.mark.parametrize("T", [1, 5, 40])
 def test_router_exact_ties(T):
     """Identical router rows give exactly equal logits; the reference breaks the
