@@ -355,11 +355,17 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   float *wts = d_w ? d_w : l->wts;
   const int H = d.hidden, E = d.n_experts, k = d.top_k, I = d.moe_inter, Is = d.shared_inter;
 
-  if (use_mfma(l, T)) {
-    // batched path: exact router and selection, then dispatch, grouped GEMMs, combine
+  // routing for T > 32: the exact sequential logits, softmax and selection
+  auto route_many = [&]() -> qmoe_status {
     STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
     STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st),
           "softmax/select launch");
+    return QMOE_OK;
+  };
+
+  if (use_mfma(l, T)) {
+    // batched path: exact routing, then dispatch, grouped GEMMs, combine
+    if (qmoe_status rs = route_many()) return rs;
     PrefillArgs pa{};
     pa.T = T;
     pa.H = H;
@@ -415,9 +421,7 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   } else if (cert) {
     STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, d_out, st), "router launch");
   } else {
-    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
-    STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st),
-          "softmax/select launch");
+    if (qmoe_status rs = route_many()) return rs;
     HIP_TRY(l, launch_zero(d_out, (int64_t)T * H, st), "zero launch");
   }
   FusedArgs f{};
@@ -783,6 +787,25 @@ qmoe_status qmoe_dequant_debug(qmoe_layer *l, int32_t which, int32_t expert, flo
   if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
   (void)hipFree(tmp);
   if (e != hipSuccess) return hip_fail(l, e, "dequant_debug");
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_router_bounds_debug(qmoe_layer *l, const float *x, int32_t T, double *sb_out) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (!x || !sb_out || T <= 0) return fail(l, QMOE_ERR_INVALID, "null pointer or T <= 0");
+  if (!l->has_router) return fail(l, QMOE_ERR_STATE, "router not uploaded");
+  if (T > kMaxGemvTokens || !router_certified_supported(l->router))
+    return fail(l, QMOE_ERR_UNSUPPORTED, "no certified router for this T and router format");
+  if ((s = ensure_workspace(l, T, l->stream)) != QMOE_OK) return s;
+  const size_t nx = (size_t)T * l->d.hidden, nsb = (size_t)T * l->d.n_experts * 2;
+  hipError_t e = hipMemcpyAsync(l->xbuf, x, nx * 4, hipMemcpyHostToDevice, l->stream);
+  if (e == hipSuccess) e = launch_router_sb(l->xbuf, T, l->router, l->sb, nullptr, l->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(sb_out, l->sb, nsb * 8, hipMemcpyDeviceToHost, l->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
+  if (e != hipSuccess) return hip_fail(l, e, "router_bounds_debug");
   return QMOE_OK;
 }
 

@@ -135,6 +135,88 @@ __device__ inline void widen_chunk(const uint4 raw, uint16_t scale, float (&wv)[
   }
 }
 
+// The reference's logit of one router row against x in LDS: the sequential
+// f32 sum of model/tensors.go:77-89 (model/model.go:167-176,
+// model/moe.go:159-162), streaming the row in 16-byte chunks, eight at a
+// time, the next eight in flight while the current ones are widened and
+// summed.
+template <int FMT>
+__device__ float exact_row_logit(const float *__restrict__ xs, int H, const uint8_t *__restrict__ row,
+                                 const uint16_t *__restrict__ srow) {
+#pragma clang fp contract(off)
+  constexpr int EPC = Chunk<FMT>::kElems;
+  const int nch = H / EPC;
+  uint4 raw[2][8];
+  uint16_t sc[2][8];
+  auto fetch = [&](int g, int c0) {
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const int ch = min(c0 + c, nch - 1);
+      raw[g][c] = *reinterpret_cast<const uint4 *>(row + (size_t)ch * 16);
+      sc[g][c] = fmt_quant(FMT) ? srow[(ch * EPC) / kGroup] : (uint16_t)0;
+    }
+  };
+  float L = 0.0f;
+  fetch(0, 0);
+  for (int c0 = 0; c0 < nch; c0 += 16) {
+    fetch(1, c0 + 8);
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+      if (c0 + c < nch) {
+        float wv[EPC];
+        widen_chunk<FMT>(raw[0][c], sc[0][c], wv);
+#pragma unroll
+        for (int i = 0; i < EPC; i++) L = L + xs[(c0 + c) * EPC + i] * wv[i];
+      }
+    fetch(0, c0 + 16);
+#pragma unroll
+    for (int c = 0; c < 8; c++)
+      if (c0 + 8 + c < nch) {
+        float wv[EPC];
+        widen_chunk<FMT>(raw[1][c], sc[1][c], wv);
+#pragma unroll
+        for (int i = 0; i < EPC; i++) L = L + xs[(c0 + 8 + c) * EPC + i] * wv[i];
+      }
+  }
+  return L;
+}
+
+// Exact logits of one token for every expert into lt, by the first nthreads
+// threads of the block (the certification's last resort): a bf16 router, the
+// format of every certified router in practice, streams its rows; the other
+// formats take a plain element loop (same sums, fewer registers).
+__device__ __forceinline__ void exact_logits_block(const float *__restrict__ xs, int H, const uint8_t *__restrict__ w,
+                                                   const uint16_t *__restrict__ sc, int fmt, int E,
+                                                   float *__restrict__ lt, int nthreads) {
+#pragma clang fp contract(off)
+  const int64_t row_bytes = fmt_matrix_bytes(fmt, 1, H);
+  for (int e = threadIdx.x; e < E; e += nthreads) {
+    const uint8_t *row = w + (size_t)e * row_bytes;
+    const uint16_t *srow = fmt_quant(fmt) ? sc + (size_t)e * (H / kGroup) : nullptr;
+    if (fmt == kBF16) {
+      lt[e] = exact_row_logit<kBF16>(xs, H, row, nullptr);
+      continue;
+    }
+    float acc = 0.0f;
+    if (fmt == kF32) {
+      for (int h = 0; h < H; h++) acc = acc + xs[h] * reinterpret_cast<const float *>(row)[h];
+    } else if (fmt == kINT8) {
+      for (int h = 0; h < H; h++) {
+        const float wv = (float)(int8_t)row[h] * f16_to_f32(srow[h / kGroup]);
+        acc = acc + xs[h] * wv;
+      }
+    } else {
+      for (int h = 0; h < H; h++) {
+        const uint8_t b = row[h / 2];
+        const int nib = (h % 2 == 0) ? (b >> 4) : (b & 0xf);
+        const float wv = ((float)nib - 8.0f) * f16_to_f32(srow[h / kGroup]);
+        acc = acc + xs[h] * wv;
+      }
+    }
+    lt[e] = acc;
+  }
+}
+
 // Rescue of a failed certification (one full wavefront): the candidates
 // whose upper bound reaches the k-th selected one's lower bound (less the f32
 // rounding of the round keys) -- the only ones that can be in the top k or
@@ -150,7 +232,6 @@ __device__ bool refine_select(double (&S)[NJ], double (&B)[NJ], double kth_lo, i
                               const uint16_t *__restrict__ rs, int *list, int32_t *g_ids, float *g_w, int *s_ids,
                               float *s_w) {
 #pragma clang fp contract(off)
-  constexpr int EPC = Chunk<FMT>::kElems;
   const int lane = threadIdx.x & 63;
   const double thr = kth_lo - fabs(kth_lo) * 0x1p-20 - 0x1p-60;
   bool in[NJ];
@@ -172,27 +253,8 @@ __device__ bool refine_select(double (&S)[NJ], double (&B)[NJ], double kth_lo, i
   float L = 0.0f;
   if (lane < n) {
     const int e = list[lane];
-    const uint8_t *row = rw + (size_t)e * fmt_matrix_bytes(FMT, 1, H);
-    const uint16_t *srow = fmt_quant(FMT) ? rs + (size_t)e * (H / kGroup) : nullptr;
-    const int nch = H / EPC;
-    for (int c0 = 0; c0 < nch; c0 += 8) {  // eight raw 16-byte chunks in flight, widened one at a time
-      uint4 raw[8];
-      uint16_t sc[8];
-#pragma unroll
-      for (int c = 0; c < 8; c++) {
-        const int ch = min(c0 + c, nch - 1);
-        raw[c] = *reinterpret_cast<const uint4 *>(row + (size_t)ch * 16);
-        sc[c] = fmt_quant(FMT) ? srow[(ch * EPC) / kGroup] : (uint16_t)0;
-      }
-#pragma unroll
-      for (int c = 0; c < 8; c++)
-        if (c0 + c < nch) {
-          float wv[EPC];
-          widen_chunk<FMT>(raw[c], sc[c], wv);
-#pragma unroll
-          for (int i = 0; i < EPC; i++) L = L + xs[(c0 + c) * EPC + i] * wv[i];
-        }
-    }
+    L = exact_row_logit<FMT>(xs, H, rw + (size_t)e * fmt_matrix_bytes(FMT, 1, H),
+                             fmt_quant(FMT) ? rs + (size_t)e * (H / kGroup) : nullptr);
   }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
 #pragma unroll

@@ -387,38 +387,5 @@ __device__ __forceinline__ bool certified_select_nj(const double *__restrict__ s
     }                             \
   } while (0)
 
-// Exact sequential logits (model/tensors.go:77-89, model/model.go:167-176,
-// model/moe.go:159-162) of one token for every expert, computed by the whole
-// first nthreads threads of the block into lt, with a run-time format switch
-// (slow path only).
-__device__ __forceinline__ void exact_logits_block(const float *__restrict__ xs, int H, const uint8_t *__restrict__ w,
-                                                   const uint16_t *__restrict__ sc, int fmt, int E,
-                                                   float *__restrict__ lt, int nthreads) {
-#pragma clang fp contract(off)
-  const int64_t row_bytes = fmt_matrix_bytes(fmt, 1, H);
-  for (int e = threadIdx.x; e < E; e += nthreads) {
-    const uint8_t *row = w + (size_t)e * row_bytes;
-    const uint16_t *srow = fmt_quant(fmt) ? sc + (size_t)e * (H / kGroup) : nullptr;
-    float acc = 0.0f;
-    if (fmt == kF32) {
-      for (int h = 0; h < H; h++) acc = acc + xs[h] * reinterpret_cast<const float *>(row)[h];
-    } else if (fmt == kBF16) {
-      for (int h = 0; h < H; h++) acc = acc + xs[h] * bf16_to_f32(reinterpret_cast<const uint16_t *>(row)[h]);
-    } else if (fmt == kINT8) {
-      for (int h = 0; h < H; h++) {
-        const float wv = (float)(int8_t)row[h] * f16_to_f32(srow[h / kGroup]);
-        acc = acc + xs[h] * wv;
-      }
-    } else {
-      for (int h = 0; h < H; h++) {
-        const uint8_t b = row[h / 2];
-        const int nib = (h % 2 == 0) ? (b >> 4) : (b & 0xf);
-        const float wv = ((float)nib - 8.0f) * f16_to_f32(srow[h / kGroup]);
-        acc = acc + xs[h] * wv;
-      }
-    }
-    lt[e] = acc;
-  }
-}
 
 }  // namespace qmoe

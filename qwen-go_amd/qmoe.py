@@ -71,6 +71,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_profile_read": ([vp, vp, vp, i32], i32),
         "qmoe_router_fallbacks": ([vp, vp], i32),
         "qmoe_router_rescues": ([vp, vp], i32),
+        "qmoe_router_bounds_debug": ([vp, vp, i32, vp], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -85,7 +86,7 @@ def exported_symbols() -> list[str]:
             "qmoe_set_router", "qmoe_set_experts", "qmoe_set_shared", "qmoe_quantize_experts",
             "qmoe_quantize_device", "qmoe_forward", "qmoe_forward_device", "qmoe_dequant_debug",
             "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks",
-            "qmoe_router_rescues"]
+            "qmoe_router_rescues", "qmoe_router_bounds_debug"]
 
 
 (STAGE_ROUTER, STAGE_SELECT, STAGE_GATE_UP, STAGE_SHARED_GATE_UP, STAGE_DOWN, STAGE_FUSED, STAGE_DISPATCH,
@@ -231,6 +232,15 @@ class MoeLayer:
         n = ctypes.c_int64()
         self._check(self.lib.qmoe_router_fallbacks(self.h, ctypes.byref(n)))
         return int(n.value)
+
+    def router_bounds(self, x: np.ndarray) -> np.ndarray:
+        """{S, B} per (token, expert) from the certified router forward uses
+        for these tokens: (T, E, 2) float64."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = x.shape[0]
+        out = np.empty((T, self.cfg.n_experts, 2), dtype=np.float64)
+        self._check(self.lib.qmoe_router_bounds_debug(self.h, x.ctypes.data, T, out.ctypes.data))
+        return out
 
     def router_rescues(self) -> int:
         """Tokens whose first certification failed and was rescued by exact

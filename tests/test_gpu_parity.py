@@ -242,6 +242,50 @@ def test_router_tile_shapes(rf, H, T):
     check_layer(cfg, hw, x)
 
 
+BOUND_CASES = [
+    # (hidden, experts, router fmt, T, router scale)
+    (2048, 128, qmoe.BF16, 5, 1.0),
+    (2048, 128, qmoe.BF16, 9, 4.0),
+    (2048, 512, qmoe.BF16, 6, 4.0),
+    (1024, 64, qmoe.INT8G32, 7, 1.0),
+    (1024, 64, qmoe.INT4G32, 5, 1.0),
+    (512, 32, qmoe.F32, 8, 1.0),
+]
+
+
+@pytest.mark.parametrize("H,E,rf,T,rs", BOUND_CASES, ids=lambda v: str(v))
+def test_router_bounds_contain_reference_logits(H, E, rf, T, rs):
+    """Every reference logit (the sequential f32 matvec of model/tensors.go,
+    computed by the oracle) lies in [S - B, S + B] of the certified decode
+    router,
+    for ordinary rows and for rows of zeros, huge, tiny and mixed magnitudes;
+    and the bound is tight enough to be useful (median B below 1e-4 of the
+    logits' spread: closer pairs go to the exact-logit rescue)."""
+    cfg = qmoe.LayerConfig(H, E, 8, 64, 0, E, rf, qmoe.BF16, qmoe.BF16, "bounds")
+    announce(f"router bounds H={H} E={E} fmt={rf} T={T}")
+    hw = qmoe.synthetic_weights(cfg, H + T, quantizer=oracle.host_quantizer, router_scale=rs)
+    x = qmoe.synthetic_tokens(cfg, T, H + T)
+    x[0] = 0.0
+    x[1] *= 1e4
+    x[2] *= 1e-20
+    x[3, : H // 2] *= 1e3
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        sb = layer.router_bounds(x)
+    finally:
+        layer.close()
+    scales = oracle.f16_to_f32(hw.router_s) if hw.router_s is not None else None
+    L = np.stack([oracle.matvec(rf, hw.router, scales, x[t], E, H) for t in range(T)]).astype(np.float64)
+    S, B = sb[..., 0], sb[..., 1]
+    assert np.all(np.isfinite(S)) and np.all(B >= 0)
+    dev = np.abs(L - S)
+    assert np.all(dev <= B), f"bound violated at {np.argwhere(dev > B)[:5]}, worst {np.max(dev - B):.3e}"
+    spread = np.median(np.std(L[4:], axis=1))
+    print(f"median B {np.median(B[4:]):.3e}, median |L - S| {np.median(dev[4:]):.3e}, logit spread {spread:.3f}")
+    assert np.median(B[4:]) < 1e-4 * spread, (np.median(B[4:]), spread)
+
+
 @pytest.mark.parametrize("T", [1, 5, 12])
 def test_router_near_tie_rescue(T):
     """Two router rows one bf16 ulp apart at their largest weight, where x is
@@ -308,7 +352,7 @@ def test_router_exact_ties(T):
     assert list(ids[0][:2]) in ([3, 5], [2, 9]), ids[0]
     assert rel_err(out, ref) <= tol
     if T <= 32:
-        assert fb >= T  # every token hit a tie
+        assert fb >= T  # every token hit a tie, which only the exact path settles
 
 
 @pytest.mark.parametrize("scope_tag", ["E", "k"])
