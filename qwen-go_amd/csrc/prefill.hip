@@ -156,23 +156,54 @@ __global__ void __launch_bounds__(kDispatchThreads)
   }
 }
 
-// Every (token, rank) pair into its expert's slot range -- one pair per
-// thread, spread over the whole device (the stores land anywhere); then the
-// shared expert's slots in token order.
+// Every (token, rank) pair into its expert's slot range, kScatterPairs pairs
+// per workgroup: each pair takes a rank among the workgroup's pairs of its
+// expert (LDS atomics), the workgroup reserves each expert's run with one
+// global atomic on its cursor, and the pairs land at run start + rank.  A hot
+// expert's cursor then sees one atomic per workgroup instead of one per pair.
+// The order of slots within an expert is free: each row of the GEMMs depends
+// on its own slot only.  Workgroups past the pairs write the shared expert's
+// slots in token order.
+constexpr int kScatterPairs = 1024;
+
 __global__ void __launch_bounds__(256) scatter_kernel(const int32_t *__restrict__ ids, const float *__restrict__ wts,
-                                                      const float *__restrict__ sg, int T, int k, int with_shared,
-                                                      PrefillPlan p) {
-  const int n = T * k;
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < n) {
-    const int slot = atomicAdd(&p.cursor[ids[i]], 1);
+                                                      const float *__restrict__ sg, int T, int k, int E,
+                                                      int with_shared, PrefillPlan p) {
+  __shared__ int lcnt[1024], lbase[1024];  // E <= 1024
+  const int n = T * k, tid = threadIdx.x;
+  const int nbr = (n + kScatterPairs - 1) / kScatterPairs;
+  if ((int)blockIdx.x >= nbr) {
+    const int t = ((int)blockIdx.x - nbr) * 256 + tid;
+    if (with_shared && t < T) {
+      p.tok[n + t] = t;
+      p.wslot[n + t] = sg[t];
+    }
+    return;
+  }
+  for (int e = tid; e < E; e += 256) lcnt[e] = 0;
+  __syncthreads();
+  constexpr int PPT = kScatterPairs / 256;
+  int id[PPT], rank[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; j++) {
+    const int i = blockIdx.x * kScatterPairs + j * 256 + tid;
+    id[j] = i < n ? ids[i] : -1;
+    rank[j] = id[j] >= 0 ? atomicAdd(&lcnt[id[j]], 1) : 0;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) {
+    const int c = lcnt[e];
+    lbase[e] = c ? atomicAdd(&p.cursor[e], c) : 0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PPT; j++) {
+    if (id[j] < 0) continue;
+    const int i = blockIdx.x * kScatterPairs + j * 256 + tid;
+    const int slot = lbase[id[j]] + rank[j];
     p.tok[slot] = i / k;
     p.wslot[slot] = wts[i];
     p.slot_of[i] = slot;
-  } else if (with_shared && i - n < T) {
-    const int t = i - n;
-    p.tok[n + t] = t;
-    p.wslot[n + t] = sg[t];
   }
 }
 
@@ -610,9 +641,8 @@ hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, con
   else if (n <= 48 * kDispatchThreads) L(48);
   else L(0);
 #undef L
-  const int items = n + (with_shared ? a.T : 0);
-  QMOE_LAUNCH(scatter_kernel, dim3((items + 255) / 256), dim3(256), 0, st, ids, wts, sg, a.T, a.k, (int)with_shared,
-              a.p);
+  const int blocks = (n + kScatterPairs - 1) / kScatterPairs + (with_shared ? (a.T + 255) / 256 : 0);
+  QMOE_LAUNCH(scatter_kernel, dim3(blocks), dim3(256), 0, st, ids, wts, sg, a.T, a.k, a.E, (int)with_shared, a.p);
   return hipGetLastError();
 }
 
