@@ -172,13 +172,16 @@ qmoe_status qmoe_profile_read(qmoe_layer *layer, double *stage_ms, int64_t *stag
  * with the exact sequential path.  Synchronises the device. */
 qmoe_status qmoe_router_fallbacks(qmoe_layer *layer, int64_t *count);
 
-/* Diagnostics with no reference counterpart: the certified decode router's
- * partials for T <= 32 tokens x (host, T x hidden f32) -- sb_out (host,
- * T x n_experts x 2 doubles) receives {S, B} per (token, expert), where the
- * reference's f32 logit is guaranteed to lie in [S - B, S + B] (S: the f64
- * sum of the f32 products; B: the bound on the sequential f32 sum).
- * QMOE_ERR_UNSUPPORTED for T > 32 (forward routes those exactly) or a router
- * format the certified router does not take.  Synchronises the device. */
+/* Diagnostics with no reference counterpart: the certified router's partials
+ * for tokens x (host, T x hidden f32) -- sb_out (host, T x n_experts x 2
+ * doubles) receives {S, B} per (token, expert), where the reference's f32
+ * logit is guaranteed to lie in [S - B, S + B].  T <= 32: the decode router
+ * (S: the f64 sum of the f32 products; B: the bound on the sequential f32
+ * sum).  T > 32: the matrix-core router (bf16 router, hidden a multiple of 64
+ * and at most 8192; S: f32 block sums of exact bf16 pieces of x; B also
+ * bounds their roundings), which forward uses when T x n_experts >= 2^20.
+ * QMOE_ERR_UNSUPPORTED for a router format or size neither takes.
+ * Synchronises the device. */
 qmoe_status qmoe_router_bounds_debug(qmoe_layer *layer, const float *x, int32_t T, double *sb_out);
 
 /* Diagnostics with no reference counterpart: the number of tokens, since

@@ -62,6 +62,8 @@ struct qmoe_layer {
   float *logits = nullptr, *wts = nullptr;
   float *xbuf = nullptr, *obuf = nullptr;
   double *sb = nullptr;
+  uint16_t *xp = nullptr;  // (4, T, H) bf16 parts of x
+  int *fbl = nullptr;      // {count, tokens} for the exact routing path
   int32_t *ids = nullptr;
   // batched (MFMA) path buffers, present when ws_mfma
   bool ws_mfma = false;
@@ -265,6 +267,9 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Token counts above this run the batched MFMA path when its formats allow.
 constexpr int kMaxGemvTokens = 32;
+// Tokens x experts from which the batched routing uses the matrix-core
+// partials (the exact router's cost grows with T * E * H on the VALU).
+constexpr int64_t kCertManyMin = (int64_t)1 << 20;
 
 bool use_mfma(const qmoe_layer *l, int T) {
   const qmoe_desc &d = l->d;
@@ -285,6 +290,8 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_x = take((size_t)nT * d.hidden * 4);
   size_t o_o = take((size_t)nT * d.hidden * 4);
   size_t o_sb = take((size_t)nT * d.n_experts * 16);
+  size_t o_xp = take((size_t)nT * d.hidden * 8);  // x split into bf16 parts for the batched certified router
+  size_t o_fbl = take((size_t)(nT + 1) * 4);      // tokens queued for the exact routing path
   const bool want_mfma = mfma || l->ws_mfma;
   const size_t pairs = (size_t)nT * d.top_k, slots = pairs + (size_t)nT;
   const int bm = prefill_tile_slots(d.expert_fmt);
@@ -326,6 +333,8 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   l->xbuf = (float *)(b + o_x);
   l->obuf = (float *)(b + o_o);
   l->sb = (double *)(b + o_sb);
+  l->xp = (uint16_t *)(b + o_xp);
+  l->fbl = (int *)(b + o_fbl);
   l->ws_mfma = want_mfma;
   if (want_mfma) {
     l->xb = (uint16_t *)(b + o_xb);
@@ -355,8 +364,19 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   float *wts = d_w ? d_w : l->wts;
   const int H = d.hidden, E = d.n_experts, k = d.top_k, I = d.moe_inter, Is = d.shared_inter;
 
-  // routing for T > 32: the exact sequential logits, softmax and selection
+  // routing for T > 32.  Many tokens x experts with a bf16 router: bounded
+  // partials on the matrix cores, then exact logits of the candidates those
+  // leave; otherwise the exact sequential logits of every expert (VALU-bound)
+  // and the exact softmax and selection.
   auto route_many = [&]() -> qmoe_status {
+    if ((int64_t)T * E >= kCertManyMin && router_cert_mfma_supported(l->router)) {
+      STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, l->xp, l->sb, st),
+            "router partials launch");
+      STAGE(l, QMOE_STAGE_SELECT, st,
+            launch_select_candidates(d_x, T, l->router, k, l->scope, l->sb, ids, wts, l->fbl, l->fallbacks, st),
+            "candidate selection launch");
+      return QMOE_OK;
+    }
     STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
     STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st),
           "softmax/select launch");
@@ -797,12 +817,15 @@ qmoe_status qmoe_router_bounds_debug(qmoe_layer *l, const float *x, int32_t T, d
   if (s) return s;
   if (!x || !sb_out || T <= 0) return fail(l, QMOE_ERR_INVALID, "null pointer or T <= 0");
   if (!l->has_router) return fail(l, QMOE_ERR_STATE, "router not uploaded");
-  if (T > kMaxGemvTokens || !router_certified_supported(l->router))
+  const bool small = T <= kMaxGemvTokens;
+  if (small ? !router_certified_supported(l->router) : !router_cert_mfma_supported(l->router))
     return fail(l, QMOE_ERR_UNSUPPORTED, "no certified router for this T and router format");
   if ((s = ensure_workspace(l, T, l->stream)) != QMOE_OK) return s;
   const size_t nx = (size_t)T * l->d.hidden, nsb = (size_t)T * l->d.n_experts * 2;
   hipError_t e = hipMemcpyAsync(l->xbuf, x, nx * 4, hipMemcpyHostToDevice, l->stream);
-  if (e == hipSuccess) e = launch_router_sb(l->xbuf, T, l->router, l->sb, nullptr, l->stream);
+  if (e == hipSuccess)
+    e = small ? launch_router_sb(l->xbuf, T, l->router, l->sb, nullptr, l->stream)
+              : launch_router_cert_mfma(l->xbuf, T, l->router, l->xp, l->sb, l->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(sb_out, l->sb, nsb * 8, hipMemcpyDeviceToHost, l->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
   if (e != hipSuccess) return hip_fail(l, e, "router_bounds_debug");

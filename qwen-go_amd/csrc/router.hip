@@ -357,6 +357,383 @@ __global__ void __launch_bounds__(256) select_cert_kernel(const float *__restric
 
 size_t select_cert_lds_bytes(int E, int H) { return (size_t)H * 4 + (size_t)E * 4; }
 
+// ---- certified router partials for many tokens on the matrix cores (bf16
+// router, H a multiple of 64 and at most 8192)
+//
+// x is split exactly into three bf16 parts, x = x1 + x2 + x3 (truncations:
+// each remainder is exact in f32 and the last has at most 8 significant
+// bits), plus |x| rounded up to bf16.  The matrix cores then give, per
+// 64-wide k block, the block sum of the exact products x_p * w of all three
+// parts (one f32 accumulator, 192 terms) and of |x|up * |w|.  Per (token,
+// expert) the kernel keeps in f32 the running estimate S (block by block),
+// A = the sum of |S| at the block ends, and P = the running sum of the |.|
+// products, and writes {S, B} with B a rigorous bound on
+// |reference logit - S|:
+//   errS = 1.004 g193 P' + u A'                 (MFMA sums of 193 terms, the
+//                                                 running sum)
+//   sum_h |S_h| <= 64 (A' + nb errS) + 64 P' + H u P'   (prefix sums inside a
+//                                                 block bounded by the last
+//                                                 block end plus the block's
+//                                                 |products|)
+//   B = u (1 + 2Hu + 1e-9) sum_h |S_h| + u (1 + u) P' + errS + 1e-25
+// with u = 2^-24, gn = nu / (1 - nu), nb = H / 64, and A', P' the f32 sums
+// scaled up by their own rounding (and P' by the MFMA's).  The first term is
+// the reference's sequential f32 sum (model/tensors.go:77-89) as the decode
+// router bounds it; u P' covers its product roundings.  Pieces: planes of T*H
+// bf16, in the order x1, x2, x3, |x|up.
+constexpr int kCertPitch = 72;  // LDS row pitch of a 64-wide bf16 piece row (no bank conflicts)
+
+__global__ void __launch_bounds__(256) x_pieces_kernel(const float *__restrict__ x, int64_t n,
+                                                       uint16_t *__restrict__ xp) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i0 >= n) return;
+  const float4 v0 = *reinterpret_cast<const float4 *>(x + i0), v1 = *reinterpret_cast<const float4 *>(x + i0 + 4);
+  const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+  uint32_t q[4][4];
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    uint32_t h[4][2];
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+      const uint32_t b = __float_as_uint(v[j + d]);
+      const float r1 = v[j + d] - __uint_as_float(b & 0xffff0000u);  // exact
+      const uint32_t b1 = __float_as_uint(r1);
+      const float r2 = r1 - __uint_as_float(b1 & 0xffff0000u);        // exact, at most 8 significant bits
+      h[0][d] = b >> 16;
+      h[1][d] = b1 >> 16;
+      h[2][d] = __float_as_uint(r2) >> 16;
+      h[3][d] = ((b & 0x7fffffffu) + 0xffffu) >> 16;                    // |x| rounded up
+    }
+#pragma unroll
+    for (int p = 0; p < 4; p++) q[p][j / 2] = h[p][0] | (h[p][1] << 16);
+  }
+#pragma unroll
+  for (int p = 0; p < 4; p++)
+    *reinterpret_cast<uint4 *>(xp + (size_t)p * n + i0) = make_uint4(q[p][0], q[p][1], q[p][2], q[p][3]);
+}
+
+typedef __bf16 cert_bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float cert_f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+// native 16-byte vectors: the HIP uint4 struct is copied through private
+// memory in these register arrays
+typedef unsigned int cert_u32x4 __attribute__((ext_vector_type(4)));
+
+// The MFMAs of one 64-wide k block (four 16-wide steps, the three x parts
+// against w into acc[0], |x|up against |w| into acc[1]); the first step
+// takes a zero accumulator operand, so acc needs no clearing between blocks.
+__device__ __forceinline__ void cert_mfma_block(const uint16_t *as, int l32, int hi, const cert_u32x4 (&wc)[4],
+                                                cert_f32x16 (&acc)[2]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++) {
+    const int ko = l32 * kCertPitch + 16 * ks + 8 * hi;
+    const cert_u32x4 wa = wc[ks] & 0x7fff7fffu;
+    const cert_bf16x8 bw = __builtin_bit_cast(cert_bf16x8, wc[ks]);
+    const cert_bf16x8 bwa = __builtin_bit_cast(cert_bf16x8, wa);
+    cert_bf16x8 av[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) av[p] = *reinterpret_cast<const cert_bf16x8 *>(as + p * 32 * kCertPitch + ko);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[0], bw, ks ? acc[0] : cert_f32x16{}, 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[3], bwa, ks ? acc[1] : cert_f32x16{}, 0, 0, 0);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[1], bw, acc[0], 0, 0, 0);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[2], bw, acc[0], 0, 0, 0);
+  }
+}
+
+// A block's sums folded into S, A, P.
+__device__ __forceinline__ void cert_fold(cert_f32x16 (&acc)[2], float (&S)[16], float (&A)[16], float (&P)[16]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    S[i] = S[i] + acc[0][i];
+    A[i] = A[i] + fabsf(S[i]);
+    P[i] = P[i] + acc[1][i];
+  }
+}
+
+// One workgroup: 32 tokens x 128 experts, wave v the experts 128 bx + 32 v +
+// (lane % 32).  The 32 x 64 piece tiles of a k block are staged in LDS once
+// for the four waves (double buffered, one barrier per block); each wave keeps
+// its router fragments in registers, loaded two blocks ahead.
+__global__ void __launch_bounds__(256, 1) router_cert_mfma_kernel(const uint16_t *__restrict__ xp, int T, int H,
+                                                               const uint16_t *__restrict__ w, int E,
+                                                               double *__restrict__ sb) {
+#pragma clang fp contract(off)
+  __shared__ __align__(16) uint16_t at[2][4][32 * kCertPitch];
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t0 = blockIdx.y * 32;
+  const int ew0 = blockIdx.x * 128 + wv * 32;  // first expert of this wave (uniform)
+  const bool live = ew0 < E;
+  const int e = ew0 + l32;
+  const int64_t plane = (int64_t)T * H;
+  const uint16_t *wrow = w + (size_t)min(e, E - 1) * H + 8 * hi;
+  // A staging: thread -> piece tid / 64, row (tid % 64) / 2, k half tid % 2
+  const int sp = tid >> 6, sr = (tid & 63) >> 1, sh = tid & 1;
+  const uint16_t *asrc = xp + (size_t)sp * plane + (size_t)min(t0 + sr, T - 1) * H + sh * 32;
+  // two register sets, loaded two blocks ahead (block indices clamped; the
+  // loads past the end are never used)
+  const int nb = H / 64;
+  cert_u32x4 an0[4], wn0[4], an1[4], wn1[4];  // the two register sets, named apart
+  cert_f32x16 acc[2];
+  float S[16], A[16], P[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) S[i] = A[i] = P[i] = 0.0f;
+  // block blk's loads into register set (AN, WN) (block clamped: loads past
+  // the end are never used)
+#define CERT_LOAD(AN, WN, blk)                                                                  \
+  do {                                                                                          \
+    const int k0_ = min((blk), nb - 1) * 64;                                                    \
+    _Pragma("unroll") for (int i_ = 0; i_ < 4; i_++)                                            \
+        AN[i_] = *reinterpret_cast<const cert_u32x4 *>(asrc + k0_ + 8 * i_);                     \
+    _Pragma("unroll") for (int ks_ = 0; ks_ < 4; ks_++)                                         \
+        WN[ks_] = *reinterpret_cast<const cert_u32x4 *>(wrow + k0_ + 16 * ks_);                  \
+  } while (0)
+  // block blk from register set (AN, WN) through LDS buffer BUF, then the
+  // set's loads for block blk + 2
+#define CERT_BLOCK(AN, WN, BUF, blk)                                                            \
+  do {                                                                                          \
+    _Pragma("unroll") for (int i_ = 0; i_ < 4; i_++)                                            \
+        *reinterpret_cast<cert_u32x4 *>(&at[BUF][sp][sr * kCertPitch + sh * 32] + 8 * i_) = AN[i_]; \
+    cert_u32x4 wc_[4];                                                                          \
+    _Pragma("unroll") for (int ks_ = 0; ks_ < 4; ks_++) wc_[ks_] = WN[ks_];                     \
+    CERT_LOAD(AN, WN, (blk) + 2);                                                               \
+    __syncthreads();                                                                            \
+    if (live) {                                                                                 \
+      cert_mfma_block(&at[BUF][0][0], l32, hi, wc_, acc);                                       \
+      cert_fold(acc, S, A, P);                                                                  \
+    }                                                                                           \
+  } while (0)
+  CERT_LOAD(an0, wn0, 0);
+  CERT_LOAD(an1, wn1, 1);
+  for (int b = 0; b < nb; b += 2) {
+    CERT_BLOCK(an0, wn0, 0, b);
+    if (b + 1 < nb) CERT_BLOCK(an1, wn1, 1, b + 1);
+  }
+#undef CERT_BLOCK
+#undef CERT_LOAD
+  if (!live || e >= E) return;
+  const double u = 0x1p-24, g65 = 65.0 * u / (1.0 - 65.0 * u), g193 = 193.0 * u / (1.0 - 193.0 * u);
+  const double fs = 1.0 + 2.0 * nb * u;  // an f32 running sum of nb terms
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int t = t0 + 8 * (i >> 2) + 4 * hi + (i & 3);
+    if (t >= T) continue;
+    const double Pp = (double)P[i] * fs * (1.0 + 2.0 * g65), Ap = (double)A[i] * fs;
+    const double errS = 1.004 * g193 * Pp + u * Ap;
+    const double sumSh = 64.0 * (Ap + nb * errS) + 64.0 * Pp + H * u * Pp;
+    const double Bv = u * (1.0 + 2.0 * H * u + 1e-9) * sumSh + u * (1.0 + u) * Pp + errS + 1e-25;
+    *reinterpret_cast<double2 *>(sb + ((size_t)t * E + e) * 2) = make_double2((double)S[i], Bv);
+  }
+}
+
+bool router_cert_mfma_supported(const DevMat &router) {
+  return router.fmt == kBF16 && router.cols % 64 == 0 && router.cols <= 8192 && router.rows <= kMaxE;
+}
+
+hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, uint16_t *xp, double *sb,
+                                   hipStream_t st) {
+  const int H = router.cols, E = router.rows;
+  const int64_t n = (int64_t)T * H;
+  QMOE_LAUNCH(x_pieces_kernel, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0, st, x, n, xp);
+  QMOE_LAUNCH(router_cert_mfma_kernel, dim3((E + 127) / 128, (T + 31) / 32), dim3(256), 0, st, xp, T, H,
+              reinterpret_cast<const uint16_t *>(router.w), E, sb);
+  return hipGetLastError();
+}
+
+// Selection for many tokens from the matrix-core partials (bf16 router), one
+// wavefront per token.  lo_k = the k-th largest lower bound S - B among the
+// candidates of the scope; every expert whose upper bound S + B reaches it
+// (the true top k are among them: k experts have logits >= lo_k) gets its
+// reference logit computed exactly, one per lane (the sequential f32 sum of
+// model/tensors.go:77-89 on x in LDS).  They are ranked by (logit desc, index
+// asc), which is the reference's order (tensors.go:106-121 softmax, moe.go:44-57
+// selection) whenever consecutive ranks are equal or apart by more than the
+// f32 roundings of the softmax can merge (4 ulps of their distance to the max
+// plus 2^-20), the k-th is that far above every other expert's upper bound,
+// and no probability is subnormal; otherwise, or with more than 64
+// candidates, the token is queued in fbl ({count, tokens...}) for the exact
+// path (all logits, exact softmax), which select_exact_kernel runs with a row
+// per thread.
+// Weights: e_r = fl(exp(L_r - max)) as the reference rounds it, divided by
+// the f64 softmax sum of the partials, renormalised with moe.go:63's 1e-9.
+template <int NJ>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) select_candidates_kernel(const float *__restrict__ x, DevMat router, int k,
+                                                               int scope, const double *__restrict__ sb,
+                                                               int32_t *__restrict__ ids, float *__restrict__ weights,
+                                                               int *__restrict__ fbl) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int list[64], sorted_e[64];
+  __shared__ float sorted_l[64];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const int E = router.rows, H = router.cols;
+  float *xs = reinterpret_cast<float *>(smem);
+  for (int i = lane * 4; i < H; i += 256)
+    *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(x + (size_t)t * H + i);
+  double S[NJ], B[NJ];
+  float key[NJ];  // lower bounds, rounded down to f32
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const int e = lane + 64 * j;
+    const double2 v = e < E && e < scope ? reinterpret_cast<const double2 *>(sb + (size_t)t * E * 2)[e]
+                                         : make_double2(-INFINITY, 0.0);
+    S[j] = v.x;
+    B[j] = v.y;
+    const double lo = S[j] - B[j];
+    float f = (float)lo;
+    if ((double)f > lo) {  // one f32 step down (f is finite here)
+      const uint32_t u = __float_as_uint(f);
+      f = f == 0.0f ? -0x1p-149f : __uint_as_float(f > 0.0f ? u - 1u : u + 1u);
+    }
+    key[j] = f;
+  }
+  // lo_k: k rounds of a wavefront max over each lane's sorted keys
+  float hk[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) hk[j] = key[j];
+#pragma unroll
+  for (int size = 2; size <= NJ; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+      for (int i = 0; i < NJ; i++) {
+        const int l = i ^ stride;
+        if (l > i) {
+          const bool sw = (i & size) == 0 ? hk[l] > hk[i] : hk[l] < hk[i];
+          const float a = hk[i];
+          hk[i] = sw ? hk[l] : hk[i];
+          hk[l] = sw ? a : hk[l];
+        }
+      }
+  float lo_k = -INFINITY;
+  for (int r = 0; r < k; r++) {
+    lo_k = wave_max_f32(hk[0]);
+    const uint64_t win = __ballot(hk[0] == lo_k);
+    const int wl = win ? __ffsll((unsigned long long)win) - 1 : 0;
+    if (lane == wl) {
+#pragma unroll
+      for (int j = 0; j + 1 < NJ; j++) hk[j] = hk[j + 1];
+      hk[NJ - 1] = -INFINITY;
+    }
+  }
+  // candidates (upper bound >= lo_k), compacted into list
+  bool in[NJ];
+  int n = 0;
+  double uo = -INFINITY;  // the largest upper bound among the others
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    in[j] = S[j] != -INFINITY && S[j] + B[j] >= (double)lo_k;
+    const uint64_t m = __ballot(in[j]);
+    const int idx = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (in[j] && idx < 64) list[idx] = lane + 64 * j;
+    n += __popcll(m);
+    if (!in[j] && S[j] != -INFINITY) uo = fmax(uo, S[j] + B[j]);
+  }
+  uo = wave_max_f64(uo);
+  bool ok = n <= 64 && n >= k;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  if (ok) {
+    float L = -INFINITY;
+    int ce = 0x7fffffff;
+    if (lane < n) {
+      ce = list[lane];
+      L = exact_row_logit<kBF16>(xs, H, router.w + (size_t)ce * H * 2, nullptr);
+    }
+    // rank among the candidates: (logit desc, index asc)
+    int rank = 0;
+    for (int j = 0; j < n; j++) {
+      const float Lj = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(L), j));
+      const int ej = __builtin_amdgcn_readlane(ce, j);
+      rank += (Lj > L || (Lj == L && ej < ce)) ? 1 : 0;
+    }
+    if (lane < n) {
+      sorted_l[rank] = L;
+      sorted_e[rank] = ce;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    const float Lmax = sorted_l[0];
+    bool bad = false;
+    if (lane < k) {
+      const float Lr = sorted_l[lane];
+      // the next one down: the next candidate, and below the k-th the others' upper bounds
+      const double nxt = lane + 1 < n ? (double)sorted_l[lane + 1] : -INFINITY;
+      const double below = lane == k - 1 ? fmax(nxt, uo) : nxt;
+      const double X = (double)Lmax - fmin((double)Lr, below > -INFINITY ? below : (double)Lr);
+      if (!((double)Lmax - (double)Lr < 80.0)) bad = true;
+      if (below > -INFINITY && (double)Lr != below && !((double)Lr - below > f32_4ulps(X) + 0x1p-20)) bad = true;
+      if (lane == k - 1 && uo > -INFINITY && !((double)Lr - uo > f32_4ulps(X) + 0x1p-20)) bad = true;
+    }
+    ok = !__ballot(bad);
+    if (ok) {
+      // softmax sum of the partials (the 1e-9 of moe.go:63 is relative to it)
+      double z = 0.0;
+#pragma unroll
+      for (int j = 0; j < NJ; j++)
+        if (lane + 64 * j < E) z += exp(fmin(S[j], (double)Lmax) - (double)Lmax);
+      z = wave_sum_f64(z);
+      const float er = lane < k ? (float)exp((double)(sorted_l[lane] - Lmax)) : 0.0f;
+      double esum = 0.0;
+      for (int r = 0; r < k; r++)
+        esum += (double)__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(er), r));
+      if (lane < k) {
+        ids[(size_t)t * k + lane] = sorted_e[lane];
+        weights[(size_t)t * k + lane] = (float)(((double)er / z) / (esum / z + 1e-9));
+      }
+      return;
+    }
+  }
+  // queued for the exact path
+  if (lane == 0) fbl[1 + atomicAdd(fbl, 1)] = t;
+}
+
+// The exact path for the queued tokens: every logit, a row per thread (x in
+// LDS), then the exact softmax and selection (select_exact_nj).  Workgroup b
+// takes queue entries b, b + gridDim.x, ...
+constexpr int kExactThreads = 512;
+template <int NJ>
+__global__ void __launch_bounds__(kExactThreads) select_exact_kernel(const float *__restrict__ x, DevMat router,
+                                                                     int k, int scope, const int *__restrict__ fbl,
+                                                                     int32_t *__restrict__ ids,
+                                                                     float *__restrict__ weights,
+                                                                     unsigned int *__restrict__ fallbacks) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int E = router.rows, H = router.cols, n = fbl[0];
+  float *xs = reinterpret_cast<float *>(smem);
+  float *lt = xs + H;
+  for (int q = blockIdx.x; q < n; q += gridDim.x) {
+    const int t = fbl[1 + q];
+    __syncthreads();  // the previous entry's LDS reads are done
+    for (int i = threadIdx.x; i < H; i += kExactThreads) xs[i] = x[(size_t)t * H + i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += kExactThreads)
+      lt[e] = exact_row_logit<kBF16>(xs, H, router.w + (size_t)e * H * 2, nullptr);
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      select_exact_nj<NJ>(lt, E, k, scope, ids + (size_t)t * k, weights + (size_t)t * k, nullptr, nullptr);
+      if (threadIdx.x == 0) atomicAdd(fallbacks, 1u);
+    }
+  }
+}
+
+hipError_t launch_select_candidates(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
+                                    int32_t *ids, float *weights, int *fbl, unsigned int *fallbacks,
+                                    hipStream_t st) {
+  hipError_t e = launch_zero(reinterpret_cast<float *>(fbl), 1, st);  // the queue's count (0 bits)
+  if (e != hipSuccess) return e;
+  const size_t lds = (size_t)router.cols * 4;
+#define L(NJ) QMOE_LAUNCH(select_candidates_kernel<NJ>, dim3(T), dim3(64), lds, st, x, router, k, scope, sb, ids, \
+                          weights, fbl)
+  QMOE_NJ_DISPATCH(router.rows, L);
+#undef L
+  const size_t lds2 = (size_t)router.cols * 4 + (size_t)router.rows * 4;
+  const int blocks = T < 256 ? T : 256;
+#define L(NJ) QMOE_LAUNCH(select_exact_kernel<NJ>, dim3(blocks), dim3(kExactThreads), lds2, st, x, router, k, scope, \
+                          fbl, ids, weights, fallbacks)
+  QMOE_NJ_DISPATCH(router.rows, L);
+#undef L
+  return hipGetLastError();
+}
+
 hipError_t launch_select_cert(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
                               int32_t *ids, float *weights, unsigned int *fallbacks, hipStream_t st) {
   const size_t lds = select_cert_lds_bytes(router.rows, router.cols);

@@ -141,7 +141,7 @@ __device__ inline void widen_chunk(const uint4 raw, uint16_t scale, float (&wv)[
 // time, the next eight in flight while the current ones are widened and
 // summed.
 template <int FMT>
-__device__ float exact_row_logit(const float *__restrict__ xs, int H, const uint8_t *__restrict__ row,
+__device__ __forceinline__ float exact_row_logit(const float *__restrict__ xs, int H, const uint8_t *__restrict__ row,
                                  const uint16_t *__restrict__ srow) {
 #pragma clang fp contract(off)
   constexpr int EPC = Chunk<FMT>::kElems;
@@ -227,7 +227,7 @@ __device__ __forceinline__ void exact_logits_block(const float *__restrict__ xs,
 // written) when more than 64 candidates qualify or certification still fails,
 // which takes a near or exact tie of reference logits.  list: 64 ints of LDS.
 template <int FMT, int NJ>
-__device__ bool refine_select(double (&S)[NJ], double (&B)[NJ], double kth_lo, int E, int k, int scope,
+__device__ __forceinline__ bool refine_select(double (&S)[NJ], double (&B)[NJ], double kth_lo, int E, int k, int scope,
                               const float *__restrict__ xs, int H, const uint8_t *__restrict__ rw,
                               const uint16_t *__restrict__ rs, int *list, int32_t *g_ids, float *g_w, int *s_ids,
                               float *s_w) {
