@@ -271,7 +271,7 @@ struct GemmCfg {
   static constexpr int kBPieces = kRaw / 16 / kGemmThreads;         // B pieces per thread per step
   static constexpr int kScale = kQuant ? kBPieces * kGemmThreads * 4 : 0;  // a scale dword per code piece
   static constexpr int kBSize = kRaw + kScale;                      // one B ring stage
-  static constexpr int kBStages = kQuant ? (BF == kINT8 ? 2 : 3) : 3;  // B ring: kBStages - 1 steps ahead
+  static constexpr int kBStages = 3;                                 // B ring: kBStages - 1 steps ahead
   static constexpr int kTile = kQuant ? kBStage : 16;               // one dequantised B tile
   static constexpr int kBLoads = kQuant ? 2 * kBPieces : kBPieces;  // B loads per thread per step
   static constexpr int kRB = kBM / 4;                               // slots per wave
@@ -455,7 +455,7 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
     const int kt = min(s, KT - 1);
 #pragma unroll
     for (int i = 0; i < G::kBPieces; i++) {
-      dma16_nt(bsrc[i] + (size_t)kt * kBK * fmt_bytes_x2(BF) / 2, dst + (i * kWaves + w) * 1024);
+      dma16(bsrc[i] + (size_t)kt * kBK * fmt_bytes_x2(BF) / 2, dst + (i * kWaves + w) * 1024);
       if constexpr (G::kQuant) dma4(ssrc[i] + 2 * kt, dst + G::kRaw + (i * kWaves + w) * 256);
     }
   };
