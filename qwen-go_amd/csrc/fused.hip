@@ -770,7 +770,9 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   const float w1 = nruns > 1 ? (rank1 == a.k ? s_sg : s_w[rank1]) : 0.0f;
   float *out_t = a.out + (size_t)t * H;
   // output order: the global atomics of a wave then cover 256 contiguous bytes
-  for (int j = threadIdx.x; j < H; j += kFusedBlock) {
+  const int rot = H % 64 == 0 ? (int)(blockIdx.x % (H / 64)) * 64 : 0;
+  for (int j0 = threadIdx.x; j0 < H; j0 += kFusedBlock) {
+    const int j = j0 + rot < H ? j0 + rot : j0 + rot - H;
     const int pj = pos(j / EPC, j % EPC);
     float s0 = red[pj], s1 = red[H + pj];
     if (use_burst)  // burst sums are stored in output order
