@@ -510,15 +510,9 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
   constexpr int kAfterA = (DA - 1) * G::kADma + DA * G::kBLoads;  // A of kt was issued at step kt - DA
   constexpr int kAfterB = (DB - 1) * (G::kADma + G::kBLoads);     // B of kt at step kt - DB, after its A
   constexpr int kWait = kAfterA < kAfterB ? kAfterA : kAfterB;
-  for (int kt = 0; kt < KT; kt++) {
-    wait_vm<kWait>();
+  // fragment reads of stage kt (live 32-slot blocks only)
+  auto read_frags = [&](int kt, const unsigned char *sb, bf16x8_t (&av)[G::kNRB][4], bf16x8_t (&bv)[4][4]) {
     const unsigned char *sa = aring[kt % NAS];
-    const unsigned char *sbs = bring[kt % NBS];
-    unsigned char *bt = btile[kt & 1];
-    convert(sbs, bt);
-    lds_barrier();  // stage kt visible to all; the slots refilled below were read at kt - 1
-    const unsigned char *sb = G::kQuant ? bt : sbs;
-    bf16x8_t av[G::kNRB][4], bv[4][4];
     if (nrb > 0) {
 #pragma unroll
       for (int ks = 0; ks < 4; ks++) {
@@ -530,8 +524,8 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
         for (int q = 0; q < 4; q++) bv[q][ks] = *reinterpret_cast<const bf16x8_t *>(sb + swz(brl[q], c));
       }
     }
-    issue_a(kt + DA);
-    issue_b(kt + DB);
+  };
+  auto mfmas = [&](const bf16x8_t (&av)[G::kNRB][4], const bf16x8_t (&bv)[4][4]) {
     if (nrb > 0) {
 #pragma unroll
       for (int ks = 0; ks < 4; ks++)
@@ -542,6 +536,55 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
             for (int q = 0; q < 4; q++)
               acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b][ks], bv[q][ks], acc[b][q], 0, 0, 0);
     }
+  };
+  if constexpr (G::kQuant) {
+    for (int kt = 0; kt < KT; kt++) {
+      wait_vm<kWait>();
+      const unsigned char *sbs = bring[kt % NBS];
+      unsigned char *bt = btile[kt & 1];
+      convert(sbs, bt);
+      lds_barrier();  // stage kt visible to all; the slots refilled below were read at kt - 1
+      bf16x8_t av[G::kNRB][4], bv[4][4];
+      read_frags(kt, bt, av, bv);
+      issue_a(kt + DA);
+      issue_b(kt + DB);
+      mfmas(av, bv);
+    }
+  } else {
+    // bf16: ping-pong.  Waves 0-3 (slots [0, BM/2)) and 4-7 (the other half)
+    // share the SIMDs pairwise and run half a phase apart: while one group
+    // issues its MFMAs for step kt, the other reads its fragments of a stage
+    // and issues its loads, and at each barrier they swap.  Group 0 runs
+    // M_kt | C_kt, group 1 the same one barrier later.  Hazards:
+    //   stage kt is read after the barrier that ends C_{kt-1} of group 0 and
+    //   M_{kt-1} of group 1, and each wave waits for its own pieces of stage kt
+    //   (kWait, the same count at both places) just before that barrier;
+    //   the loads issued in M_kt go to the slot of stage kt - 1, whose last
+    //   reader (group 1, M_{kt-1}) finished -- lgkmcnt(0) -- before the
+    //   barrier that starts group 0's M_kt.
+    // sched_barrier(0) keeps the compiler from moving MFMAs across phases.
+    const bool g1 = w >= kWaves / 2;
+    auto phase_barrier = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    wait_vm<kWait>();  // own pieces of stage 0
+    phase_barrier();
+    if (g1) phase_barrier();
+    for (int kt = 0; kt < KT; kt++) {
+      bf16x8_t av[G::kNRB][4], bv[4][4];
+      read_frags(kt, bring[kt % NBS], av, bv);  // M_kt
+      issue_a(kt + DA);
+      issue_b(kt + DB);
+      wait_lds_writes();  // this wave's reads of stage kt are done before the barrier
+      if (g1) wait_vm<kWait>();  // own pieces of stage kt + 1
+      phase_barrier();
+      mfmas(av, bv);  // C_kt
+      if (!g1) wait_vm<kWait>();
+      phase_barrier();
+    }
+    if (!g1) phase_barrier();
   }
   wait_vm<0>();  // no LDS-direct load may land after the workgroup ends
 
