@@ -412,12 +412,18 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
     }
   };
 
-  // A rows staged by this thread: row r = (i * kWaves + w) * 8 + lane / 8
+  // A rows staged by this thread: piece i covers rows [a_row0(i), +8), one
+  // per 8 lanes.  bf16 (ping-pong below): each half of the waves stages the
+  // half of the slots it reads; group-32: the pieces interleave all waves.
+  auto a_row0 = [&](int i) {
+    if constexpr (G::kQuant) return (i * kWaves + w) * 8;
+    else return (w / (kWaves / 2)) * (G::kBM / 2) + (i * (kWaves / 2) + w % (kWaves / 2)) * 8;
+  };
   const uint16_t *arow[G::kADma];
   int achunk[G::kADma];
 #pragma unroll
   for (int i = 0; i < G::kADma; i++) {
-    const int r = (i * kWaves + w) * 8 + (lane >> 3);
+    const int r = a_row0(i) + (lane >> 3);
     achunk[i] = (lane & 7) ^ swz_of(r);
     const int m = min(r, ti.rows - 1);
     if constexpr (KIND == kGateUp) arow[i] = a.xb + (size_t)a.p.tok[ti.slot0 + m] * H;
@@ -448,7 +454,7 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
     unsigned char *dst = aring[s % NAS];
     const int k0 = min(s, KT - 1) * kBK;
 #pragma unroll
-    for (int i = 0; i < G::kADma; i++) dma16(arow[i] + k0 + achunk[i] * 8, dst + (i * kWaves + w) * 1024);
+    for (int i = 0; i < G::kADma; i++) dma16(arow[i] + k0 + achunk[i] * 8, dst + a_row0(i) * 128);
   };
   auto issue_b = [&](int s) {
     unsigned char *dst = bring[s % NBS];
@@ -556,12 +562,15 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
     // issues its MFMAs for step kt, the other reads its fragments of a stage
     // and issues its loads, and at each barrier they swap.  Group 0 runs
     // M_kt | C_kt, group 1 the same one barrier later.  Hazards:
-    //   stage kt is read after the barrier that ends C_{kt-1} of group 0 and
-    //   M_{kt-1} of group 1, and each wave waits for its own pieces of stage kt
-    //   (kWait, the same count at both places) just before that barrier;
+    //   a group stages only its own half of the A rows, so A of stage kt
+    //   must have landed (each wave waiting for its own pieces) before the
+    //   barrier that starts the group's M_kt: at the end of its C_{kt-1};
+    //   B of stage kt is first read in group 0's M_kt, so group 1 waits for
+    //   its B pieces of stage kt at the end of its M_{kt-1} (group 0 at the
+    //   end of C_{kt-1}, together with A);
     //   the loads issued in M_kt go to the slot of stage kt - 1, whose last
-    //   reader (group 1, M_{kt-1}) finished -- lgkmcnt(0) -- before the
-    //   barrier that starts group 0's M_kt.
+    //   reader finished -- lgkmcnt(0) -- before the barrier that starts the
+    //   issuing group's M_kt (A: the group itself; B: group 1's M_{kt-1}).
     // sched_barrier(0) keeps the compiler from moving MFMAs across phases.
     const bool g1 = w >= kWaves / 2;
     auto phase_barrier = [&]() {
@@ -578,10 +587,11 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
       issue_a(kt + DA);
       issue_b(kt + DB);
       wait_lds_writes();  // this wave's reads of stage kt are done before the barrier
-      if (g1) wait_vm<kWait>();  // own pieces of stage kt + 1
+      if (g1) wait_vm<kAfterB>();  // own B pieces of stage kt + 1, which group 0 reads next
       phase_barrier();
       mfmas(av, bv);  // C_kt
-      if (!g1) wait_vm<kWait>();
+      if (g1) wait_vm<kAfterA>();  // own A pieces of stage kt + 1 (B: end of M_kt)
+      else wait_vm<kWait>();       // own A and B pieces of stage kt + 1
       phase_barrier();
     }
     if (!g1) phase_barrier();
