@@ -55,10 +55,9 @@ hipError_t launch_router_sb(const float *x, int T, const DevMat &router, double 
                             hipStream_t st);
 // Certified router partials for T > 32 on the matrix cores (bf16 router, H a
 // multiple of 64, at most 8192): the same sb as launch_router_sb, from x split
-// into exact bf16 parts (xp: T * H * 4 bf16 of workspace).
+// into exact bf16 parts inside the kernel.
 bool router_cert_mfma_supported(const DevMat &router);
-hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, uint16_t *xp, double *sb,
-                                   hipStream_t st);
+hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, double *sb, hipStream_t st);
 // Selection for T > 32 from the matrix-core partials (bf16 router): exact
 // logits of the candidates the bounds leave, ranked; the exact path for the
 // tokens whose ranks they cannot separate, queued in fbl (1 + T ints).

@@ -62,7 +62,6 @@ struct qmoe_layer {
   float *logits = nullptr, *wts = nullptr;
   float *xbuf = nullptr, *obuf = nullptr;
   double *sb = nullptr;
-  uint16_t *xp = nullptr;  // (4, T, H) bf16 parts of x
   int *fbl = nullptr;      // {count, tokens} for the exact routing path
   int32_t *ids = nullptr;
   // batched (MFMA) path buffers, present when ws_mfma
@@ -290,7 +289,6 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_x = take((size_t)nT * d.hidden * 4);
   size_t o_o = take((size_t)nT * d.hidden * 4);
   size_t o_sb = take((size_t)nT * d.n_experts * 16);
-  size_t o_xp = take((size_t)nT * d.hidden * 8);  // x split into bf16 parts for the batched certified router
   size_t o_fbl = take((size_t)(nT + 1) * 4);      // tokens queued for the exact routing path
   const bool want_mfma = mfma || l->ws_mfma;
   const size_t pairs = (size_t)nT * d.top_k, slots = pairs + (size_t)nT;
@@ -333,7 +331,6 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   l->xbuf = (float *)(b + o_x);
   l->obuf = (float *)(b + o_o);
   l->sb = (double *)(b + o_sb);
-  l->xp = (uint16_t *)(b + o_xp);
   l->fbl = (int *)(b + o_fbl);
   l->ws_mfma = want_mfma;
   if (want_mfma) {
@@ -370,7 +367,7 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   // and the exact softmax and selection.
   auto route_many = [&]() -> qmoe_status {
     if ((int64_t)T * E >= kCertManyMin && router_cert_mfma_supported(l->router)) {
-      STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, l->xp, l->sb, st),
+      STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, l->sb, st),
             "router partials launch");
       STAGE(l, QMOE_STAGE_SELECT, st,
             launch_select_candidates(d_x, T, l->router, k, l->scope, l->sb, ids, wts, l->fbl, l->fallbacks, st),
@@ -825,7 +822,7 @@ qmoe_status qmoe_router_bounds_debug(qmoe_layer *l, const float *x, int32_t T, d
   hipError_t e = hipMemcpyAsync(l->xbuf, x, nx * 4, hipMemcpyHostToDevice, l->stream);
   if (e == hipSuccess)
     e = small ? launch_router_sb(l->xbuf, T, l->router, l->sb, nullptr, l->stream)
-              : launch_router_cert_mfma(l->xbuf, T, l->router, l->xp, l->sb, l->stream);
+              : launch_router_cert_mfma(l->xbuf, T, l->router, l->sb, l->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(sb_out, l->sb, nsb * 8, hipMemcpyDeviceToHost, l->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
   if (e != hipSuccess) return hip_fail(l, e, "router_bounds_debug");

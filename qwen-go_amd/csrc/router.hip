@@ -383,33 +383,19 @@ size_t select_cert_lds_bytes(int E, int H) { return (size_t)H * 4 + (size_t)E * 
 // bf16, in the order x1, x2, x3, |x|up.
 constexpr int kCertPitch = 72;  // LDS row pitch of a 64-wide bf16 piece row (no bank conflicts)
 
-__global__ void __launch_bounds__(256) x_pieces_kernel(const float *__restrict__ x, int64_t n,
-                                                       uint16_t *__restrict__ xp) {
-  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
-  if (i0 >= n) return;
-  const float4 v0 = *reinterpret_cast<const float4 *>(x + i0), v1 = *reinterpret_cast<const float4 *>(x + i0 + 4);
-  const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-  uint32_t q[4][4];
-#pragma unroll
-  for (int j = 0; j < 8; j += 2) {
-    uint32_t h[4][2];
-#pragma unroll
-    for (int d = 0; d < 2; d++) {
-      const uint32_t b = __float_as_uint(v[j + d]);
-      const float r1 = v[j + d] - __uint_as_float(b & 0xffff0000u);  // exact
-      const uint32_t b1 = __float_as_uint(r1);
-      const float r2 = r1 - __uint_as_float(b1 & 0xffff0000u);        // exact, at most 8 significant bits
-      h[0][d] = b >> 16;
-      h[1][d] = b1 >> 16;
-      h[2][d] = __float_as_uint(r2) >> 16;
-      h[3][d] = ((b & 0x7fffffffu) + 0xffffu) >> 16;                    // |x| rounded up
-    }
-#pragma unroll
-    for (int p = 0; p < 4; p++) q[p][j / 2] = h[p][0] | (h[p][1] << 16);
-  }
-#pragma unroll
-  for (int p = 0; p < 4; p++)
-    *reinterpret_cast<uint4 *>(xp + (size_t)p * n + i0) = make_uint4(q[p][0], q[p][1], q[p][2], q[p][3]);
+// Piece p of x (as bf16 bits): x1, x2, x3 = the successive bf16
+// truncations (each remainder is exact in f32; the third has at most 8
+// significant bits), p = 3: |x| rounded up to bf16.
+template <int P>
+__device__ __forceinline__ uint32_t x_piece(float v) {
+  const uint32_t b = __float_as_uint(v);
+  if constexpr (P == 3) return ((b & 0x7fffffffu) + 0xffffu) >> 16;
+  const float r1 = v - __uint_as_float(b & 0xffff0000u);  // exact
+  if constexpr (P == 0) return b >> 16;
+  const uint32_t b1 = __float_as_uint(r1);
+  if constexpr (P == 1) return b1 >> 16;
+  const float r2 = r1 - __uint_as_float(b1 & 0xffff0000u);  // exact
+  return __float_as_uint(r2) >> 16;
 }
 
 typedef __bf16 cert_bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
@@ -439,6 +425,19 @@ __device__ __forceinline__ void cert_mfma_block(const uint16_t *as, int l32, int
   }
 }
 
+// Piece P of 8 consecutive x values, as packed bf16 pairs (element 2i in
+// the low half of word i).
+template <int P>
+__device__ __forceinline__ cert_u32x4 cert_piece8(const float4 (&v)[2]) {
+  cert_u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    out[2 * i] = x_piece<P>(v[i].x) | (x_piece<P>(v[i].y) << 16);
+    out[2 * i + 1] = x_piece<P>(v[i].z) | (x_piece<P>(v[i].w) << 16);
+  }
+  return out;
+}
+
 // A block's sums folded into S, A, P.
 __device__ __forceinline__ void cert_fold(cert_f32x16 (&acc)[2], float (&S)[16], float (&A)[16], float (&P)[16]) {
 #pragma clang fp contract(off)
@@ -452,9 +451,11 @@ __device__ __forceinline__ void cert_fold(cert_f32x16 (&acc)[2], float (&S)[16],
 
 // One workgroup: 32 tokens x 128 experts, wave v the experts 128 bx + 32 v +
 // (lane % 32).  The 32 x 64 piece tiles of a k block are staged in LDS once
-// for the four waves (double buffered, one barrier per block); each wave keeps
-// its router fragments in registers, loaded two blocks ahead.
-__global__ void __launch_bounds__(256, 1) router_cert_mfma_kernel(const uint16_t *__restrict__ xp, int T, int H,
+// for the four waves (double buffered, one barrier per block): each thread
+// loads 8 f32 of x (two blocks ahead) and stores those 8 elements of all four
+// pieces; each wave keeps its router fragments in registers, loaded two blocks
+// ahead.
+__global__ void __launch_bounds__(256, 1) router_cert_mfma_kernel(const float *__restrict__ x, int T, int H,
                                                                const uint16_t *__restrict__ w, int E,
                                                                double *__restrict__ sb) {
 #pragma clang fp contract(off)
@@ -465,15 +466,15 @@ __global__ void __launch_bounds__(256, 1) router_cert_mfma_kernel(const uint16_t
   const int ew0 = blockIdx.x * 128 + wv * 32;  // first expert of this wave (uniform)
   const bool live = ew0 < E;
   const int e = ew0 + l32;
-  const int64_t plane = (int64_t)T * H;
   const uint16_t *wrow = w + (size_t)min(e, E - 1) * H + 8 * hi;
-  // A staging: thread -> piece tid / 64, row (tid % 64) / 2, k half tid % 2
-  const int sp = tid >> 6, sr = (tid & 63) >> 1, sh = tid & 1;
-  const uint16_t *asrc = xp + (size_t)sp * plane + (size_t)min(t0 + sr, T - 1) * H + sh * 32;
+  // A staging: thread -> row tid / 8, elements [8 (tid % 8), +8) of the k block
+  const int sr = tid >> 3, sc = tid & 7;
+  const float *asrc = x + (size_t)min(t0 + sr, T - 1) * H + sc * 8;
   // two register sets, loaded two blocks ahead (block indices clamped; the
   // loads past the end are never used)
   const int nb = H / 64;
-  cert_u32x4 an0[4], wn0[4], an1[4], wn1[4];  // the two register sets, named apart
+  float4 an0[2], an1[2];
+  cert_u32x4 wn0[4], wn1[4];  // the two register sets, named apart
   cert_f32x16 acc[2];
   float S[16], A[16], P[16];
 #pragma unroll
@@ -483,8 +484,8 @@ __global__ void __launch_bounds__(256, 1) router_cert_mfma_kernel(const uint16_t
 #define CERT_LOAD(AN, WN, blk)                                                                  \
   do {                                                                                          \
     const int k0_ = min((blk), nb - 1) * 64;                                                    \
-    _Pragma("unroll") for (int i_ = 0; i_ < 4; i_++)                                            \
-        AN[i_] = *reinterpret_cast<const cert_u32x4 *>(asrc + k0_ + 8 * i_);                     \
+    _Pragma("unroll") for (int i_ = 0; i_ < 2; i_++)                                            \
+        AN[i_] = *reinterpret_cast<const float4 *>(asrc + k0_ + 4 * i_);                         \
     _Pragma("unroll") for (int ks_ = 0; ks_ < 4; ks_++)                                         \
         WN[ks_] = *reinterpret_cast<const cert_u32x4 *>(wrow + k0_ + 16 * ks_);                  \
   } while (0)
@@ -492,8 +493,10 @@ __global__ void __launch_bounds__(256, 1) router_cert_mfma_kernel(const uint16_t
   // set's loads for block blk + 2
 #define CERT_BLOCK(AN, WN, BUF, blk)                                                            \
   do {                                                                                          \
-    _Pragma("unroll") for (int i_ = 0; i_ < 4; i_++)                                            \
-        *reinterpret_cast<cert_u32x4 *>(&at[BUF][sp][sr * kCertPitch + sh * 32] + 8 * i_) = AN[i_]; \
+    *reinterpret_cast<cert_u32x4 *>(&at[BUF][0][sr * kCertPitch + sc * 8]) = cert_piece8<0>(AN); \
+    *reinterpret_cast<cert_u32x4 *>(&at[BUF][1][sr * kCertPitch + sc * 8]) = cert_piece8<1>(AN); \
+    *reinterpret_cast<cert_u32x4 *>(&at[BUF][2][sr * kCertPitch + sc * 8]) = cert_piece8<2>(AN); \
+    *reinterpret_cast<cert_u32x4 *>(&at[BUF][3][sr * kCertPitch + sc * 8]) = cert_piece8<3>(AN); \
     cert_u32x4 wc_[4];                                                                          \
     _Pragma("unroll") for (int ks_ = 0; ks_ < 4; ks_++) wc_[ks_] = WN[ks_];                     \
     CERT_LOAD(AN, WN, (blk) + 2);                                                               \
@@ -530,12 +533,9 @@ bool router_cert_mfma_supported(const DevMat &router) {
   return router.fmt == kBF16 && router.cols % 64 == 0 && router.cols <= 8192 && router.rows <= kMaxE;
 }
 
-hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, uint16_t *xp, double *sb,
-                                   hipStream_t st) {
+hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, double *sb, hipStream_t st) {
   const int H = router.cols, E = router.rows;
-  const int64_t n = (int64_t)T * H;
-  QMOE_LAUNCH(x_pieces_kernel, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0, st, x, n, xp);
-  QMOE_LAUNCH(router_cert_mfma_kernel, dim3((E + 127) / 128, (T + 31) / 32), dim3(256), 0, st, xp, T, H,
+  QMOE_LAUNCH(router_cert_mfma_kernel, dim3((E + 127) / 128, (T + 31) / 32), dim3(256), 0, st, x, T, H,
               reinterpret_cast<const uint16_t *>(router.w), E, sb);
   return hipGetLastError();
 }
