@@ -706,7 +706,8 @@ __global__ void __launch_bounds__(kExactThreads) select_exact_kernel(const float
     for (int i = threadIdx.x; i < H; i += kExactThreads) xs[i] = x[(size_t)t * H + i];
     __syncthreads();
     for (int e = threadIdx.x; e < E; e += kExactThreads)
-      lt[e] = exact_row_logit<kBF16>(xs, H, router.w + (size_t)e * H * 2, nullptr);
+      // one or two queued tokens per call: latency-bound, so 16 chunks in flight
+      lt[e] = exact_row_logit<kBF16, 16>(xs, H, router.w + (size_t)e * H * 2, nullptr);
     __syncthreads();
     if (threadIdx.x < 64) {
       select_exact_nj<NJ>(lt, E, k, scope, ids + (size_t)t * k, weights + (size_t)t * k, nullptr, nullptr);

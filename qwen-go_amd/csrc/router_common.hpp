@@ -137,20 +137,19 @@ __device__ inline void widen_chunk(const uint4 raw, uint16_t scale, float (&wv)[
 
 // The reference's logit of one router row against x in LDS: the sequential
 // f32 sum of model/tensors.go:77-89 (model/model.go:167-176,
-// model/moe.go:159-162), streaming the row in 16-byte chunks, eight at a
-// time, the next eight in flight while the current ones are widened and
-// summed.
-template <int FMT>
+// model/moe.go:159-162), streaming the row in 16-byte chunks, G at a time,
+// the next G in flight while the current ones are widened and summed.
+template <int FMT, int G = 8>
 __device__ __forceinline__ float exact_row_logit(const float *__restrict__ xs, int H, const uint8_t *__restrict__ row,
                                  const uint16_t *__restrict__ srow) {
 #pragma clang fp contract(off)
   constexpr int EPC = Chunk<FMT>::kElems;
   const int nch = H / EPC;
-  uint4 raw[2][8];
-  uint16_t sc[2][8];
+  uint4 raw[2][G];
+  uint16_t sc[2][G];
   auto fetch = [&](int g, int c0) {
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
+    for (int c = 0; c < G; c++) {
       const int ch = min(c0 + c, nch - 1);
       raw[g][c] = *reinterpret_cast<const uint4 *>(row + (size_t)ch * 16);
       sc[g][c] = fmt_quant(FMT) ? srow[(ch * EPC) / kGroup] : (uint16_t)0;
@@ -158,24 +157,24 @@ __device__ __forceinline__ float exact_row_logit(const float *__restrict__ xs, i
   };
   float L = 0.0f;
   fetch(0, 0);
-  for (int c0 = 0; c0 < nch; c0 += 16) {
-    fetch(1, c0 + 8);
+  for (int c0 = 0; c0 < nch; c0 += 2 * G) {
+    fetch(1, c0 + G);
 #pragma unroll
-    for (int c = 0; c < 8; c++)
+    for (int c = 0; c < G; c++)
       if (c0 + c < nch) {
         float wv[EPC];
         widen_chunk<FMT>(raw[0][c], sc[0][c], wv);
 #pragma unroll
         for (int i = 0; i < EPC; i++) L = L + xs[(c0 + c) * EPC + i] * wv[i];
       }
-    fetch(0, c0 + 16);
+    fetch(0, c0 + 2 * G);
 #pragma unroll
-    for (int c = 0; c < 8; c++)
-      if (c0 + 8 + c < nch) {
+    for (int c = 0; c < G; c++)
+      if (c0 + G + c < nch) {
         float wv[EPC];
         widen_chunk<FMT>(raw[1][c], sc[1][c], wv);
 #pragma unroll
-        for (int i = 0; i < EPC; i++) L = L + xs[(c0 + 8 + c) * EPC + i] * wv[i];
+        for (int i = 0; i < EPC; i++) L = L + xs[(c0 + G + c) * EPC + i] * wv[i];
       }
   }
   return L;
