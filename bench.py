@@ -104,43 +104,6 @@ def measured_traffic(workload, kernel):
 ROUTER_SCALE = {"prefill": 4.0}
 
 
-def skewed_tokens(cfg, hw, T, seed, target):
-    """x_t = z_t + c u with a fixed random unit direction u; c is chosen on the
-    host (router logits in float64) so that the busiest expert receives about
-    `target` times the median expert's load.  Returns (x, c, load stats)."""
-    rng = np.random.default_rng(seed)
-    u = rng.standard_normal(cfg.hidden)
-    u /= np.linalg.norm(u)
-    z = qmoe.synthetic_tokens(cfg, T, seed)
-    if cfg.router_fmt == qmoe.BF16:
-        r = qmoe.bf16_bits_to_f32(hw.router).astype(np.float64)
-    else:
-        r = np.asarray(hw.router, np.float64)
-    r = r.reshape(cfg.n_experts, cfg.hidden)
-    zl, ul = z.astype(np.float64) @ r.T, r @ u
-
-    def load(c):
-        lg = zl + c * ul
-        top = np.argsort(-lg, axis=1, kind="stable")[:, :cfg.top_k]
-        return np.bincount(top.reshape(-1), minlength=cfg.n_experts)
-
-    def ratio(c):
-        n = load(c)
-        return n.max() / max(np.median(n), 1.0)
-
-    lo, hi = 0.0, 64.0
-    if ratio(lo) < target:
-        for _ in range(30):
-            mid = 0.5 * (lo + hi)
-            lo, hi = (mid, hi) if ratio(mid) < target else (lo, mid)
-    c = hi if ratio(lo) < target else lo
-    n = load(c)
-    x = (z + c * u[None, :]).astype(np.float32)
-    stats = {"c": round(float(c), 3), "max_load": int(n.max()), "median_load": float(np.median(n)),
-             "min_load": int(n.min()), "experts_used": int((n > 0).sum())}
-    return x, stats
-
-
 def stage_bytes(cfg, T, ids):
     """Algorithmic HBM bytes of each kernel for one forward with routing ids."""
     H, E, k, I, Is = cfg.hidden, cfg.n_experts, cfg.top_k, cfg.moe_inter, cfg.shared_inter
@@ -247,7 +210,7 @@ def main():
     if args.workload in ROUTER_SCALE:
         xs_host, stats = [], []
         for i in range(n_x):
-            x, st = skewed_tokens(cfg, hw, T, args.seed + 1000 + i, args.skew)
+            x, st = qmoe.skewed_tokens(cfg, hw, T, args.seed + 1000 + i, args.skew)
             xs_host.append(x)
             stats.append(st)
         skew = {"target_max_over_median": args.skew, "per_x": stats}

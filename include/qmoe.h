@@ -21,6 +21,14 @@
  *                 value = nibble - 8, + fp16 scales (rows, K/32)
  *                 (model/moe.go:134-157; scales are the fp16 form that
  *                 safetensors F16 files hold, widened exactly)
+ *   QMOE_INT8G32_F32S, QMOE_INT4G32_F32S
+ *                 the same codes with f32 scales (rows, K/32): the
+ *                 quantLinear the loader builds from qwen-quant output, which
+ *                 writes its scales as F32 (cmd/qwen-quant/main.go:198-210,
+ *                 model/load.go:527-582).  Stored on the device as their exact
+ *                 f32 dequantisation float32(code) * scale (moe.go:134-157),
+ *                 which is what quantLinear.forward multiplies with
+ *                 (moe.go:159-162); 4 bytes per weight on the device.
  * For stacked experts the scale arrays are (E, rows, K/32).
  *
  * Threading: every call on one handle is serialised by a per-handle mutex, so
@@ -51,7 +59,9 @@ typedef enum {
     QMOE_F32 = 0,
     QMOE_BF16 = 1,
     QMOE_INT8G32 = 2,
-    QMOE_INT4G32 = 3
+    QMOE_INT4G32 = 3,
+    QMOE_INT8G32_F32S = 4,
+    QMOE_INT4G32_F32S = 5
 } qmoe_format;
 
 /* Layer description.  Field meanings follow model/config.go:24-27 and
@@ -87,14 +97,17 @@ const char *qmoe_last_error(const qmoe_layer *layer);
 const char *qmoe_status_string(qmoe_status s);
 
 /* Weight upload from host memory (copied, not retained), as the loader's
- * loadMLP / installQuant fill moeMLP (model/load.go:415-459, 646-664).
- * scales: fp16 bit patterns, required for the INT formats, ignored otherwise. */
-qmoe_status qmoe_set_router(qmoe_layer *layer, const void *w, const uint16_t *scales);
-qmoe_status qmoe_set_experts(qmoe_layer *layer, const void *gate_up, const uint16_t *gate_up_scales,
-                             const void *down, const uint16_t *down_scales);
-qmoe_status qmoe_set_shared(qmoe_layer *layer, const void *gate, const uint16_t *gate_scales,
-                            const void *up, const uint16_t *up_scales, const void *down,
-                            const uint16_t *down_scales, const float *shared_gate);
+ * loadMLP / installQuant fill moeMLP (model/load.go:415-459, 646-664):
+ * router = mlp.gate (or routerQuant), experts = the stacked gate_up/down,
+ * shared = shared.{gate,up,down} (or their gateQuant/upQuant/downQuant) and
+ * sharedGate.  scales: fp16 bit patterns (uint16) for QMOE_INT8G32 and
+ * QMOE_INT4G32, float32 for the *_F32S formats, ignored otherwise. */
+qmoe_status qmoe_set_router(qmoe_layer *layer, const void *w, const void *scales);
+qmoe_status qmoe_set_experts(qmoe_layer *layer, const void *gate_up, const void *gate_up_scales,
+                             const void *down, const void *down_scales);
+qmoe_status qmoe_set_shared(qmoe_layer *layer, const void *gate, const void *gate_scales,
+                            const void *up, const void *up_scales, const void *down,
+                            const void *down_scales, const float *shared_gate);
 
 /* Quantises f32 expert weights on the device into the layer's INT8G32 or
  * INT4G32 expert format: quantizeInt8 / quantizeInt4 (model/moe.go:165-217)
@@ -114,12 +127,17 @@ qmoe_status qmoe_quantize_device(int32_t bits, const float *d_w, int64_t n_mat, 
  * x (T, H) f32 in; out (T, H) f32 out.  ids (T, k) int32 and weights (T, k) f32
  * receive the selected experts and renormalised routing weights in rank
  * order; either may be NULL.  T == 0 is a no-op.  The Go seam calls it with
- * T = 1 (model/model.go:508-514). */
+ * T = 1 (model/model.go:508-514).
+ * At T = 1 the expert kernel's workgroups exchange the router partials among
+ * themselves; if that exchange times out (the device did not run them all at
+ * once) this call returns QMOE_ERR_HIP and its outputs are not valid. */
 qmoe_status qmoe_forward(qmoe_layer *layer, const float *x, int32_t T, float *out, int32_t *ids,
                          float *weights);
 
 /* Same, on device pointers, asynchronous on stream (hipStream_t; NULL = the
- * default stream).  No host synchronisation. */
+ * default stream).  No host synchronisation, so an exchange timeout of this
+ * call is reported by the next call on the handle (which then returns
+ * QMOE_ERR_HIP without running); the report clears it. */
 qmoe_status qmoe_forward_device(qmoe_layer *layer, const float *d_x, int32_t T, float *d_out,
                                 int32_t *d_ids, float *d_weights, void *stream);
 
@@ -189,6 +207,14 @@ qmoe_status qmoe_router_bounds_debug(qmoe_layer *layer, const float *x, int32_t 
  * few candidates in doubt had their exact sequential logits computed (no
  * full exact routing needed).  Synchronises the device. */
 qmoe_status qmoe_router_rescues(qmoe_layer *layer, int64_t *count);
+
+/* Diagnostics with no reference counterpart: the longest wait of the T = 1
+ * expert kernel's workgroups for each other's router partials, in ticks of
+ * the device's 100 MHz real-time counter (ticks < 0: the default, 2 ms;
+ * 0: give up at once).  A wait that gives up makes the call fail with
+ * QMOE_ERR_HIP, and every workgroup still finishes (on exact routing).  For
+ * tests of that error path. */
+qmoe_status qmoe_debug_exchange_budget(qmoe_layer *layer, int64_t ticks);
 
 /* Bytes of device memory held by the handle (weights + workspace). */
 int64_t qmoe_device_bytes(const qmoe_layer *layer);

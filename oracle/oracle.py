@@ -134,10 +134,12 @@ def quantize_f16(bits: int, w: np.ndarray):
     return codes, f32_to_f16(s)
 
 
-def host_quantizer(bits: int, w: np.ndarray, n_mat: int, rows: int, cols: int):
-    """Drop-in for qmoe.device_quantizer that runs the oracle on the CPU."""
-    return quantize_f16(bits, np.asarray(w, np.float32).reshape(n_mat, rows, cols) if n_mat > 1
-                        else np.asarray(w, np.float32).reshape(rows, cols))
+def host_quantizer(bits: int, w: np.ndarray, n_mat: int, rows: int, cols: int, f32_scales: bool = False):
+    """Drop-in for qmoe.device_quantizer that runs the oracle on the CPU.
+    f32_scales: keep the quantiser's f32 scales (what qwen-quant writes)
+    instead of rounding them to fp16."""
+    a = np.asarray(w, np.float32).reshape(n_mat, rows, cols) if n_mat > 1 else np.asarray(w, np.float32).reshape(rows, cols)
+    return quantize(bits, a) if f32_scales else quantize_f16(bits, a)
 
 
 def dequantize(bits: int, codes: np.ndarray, scales_f32: np.ndarray, rows: int, cols: int) -> np.ndarray:
@@ -188,6 +190,13 @@ def select(p: np.ndarray, k: int, scope: int):
 
 # ------------------------------------------------------------------ layer
 
+def orc_fmt(fmt: int) -> int:
+    """The oracle's format for a product format: the group-32 formats with f32
+    scales (4, 5) are the reference's quantLinear with its f32 scales, which
+    the oracle takes for every INT format."""
+    return {4: INT8G32, 5: INT4G32}.get(fmt, fmt)
+
+
 class OracleLayer:
     """Holds an OrcMoe plus the numpy arrays it points into."""
 
@@ -196,23 +205,24 @@ class OracleLayer:
         self.cfg = cfg
         self.keep = []
 
-        def sc(bits16):
-            if bits16 is None:
+        def sc(s):
+            # fp16 bit patterns are widened exactly; f32 scales are used as they are
+            if s is None:
                 return None
-            a = f16_to_f32(bits16)
+            a = np.ascontiguousarray(s, np.float32) if s.dtype == np.float32 else f16_to_f32(s)
             self.keep.append(a)
             return a
 
         def lin(fmt, w, s16, rows, cols):
             self.keep.append(w)
-            return _linear(fmt, np.ascontiguousarray(w), sc(s16), rows, cols)
+            return _linear(orc_fmt(fmt), np.ascontiguousarray(w), sc(s16), rows, cols)
 
         H, E, I, Is = cfg.hidden, cfg.n_experts, cfg.moe_inter, cfg.shared_inter
         m = OrcMoe()
         m.hidden, m.n_experts, m.top_k, m.inter, m.shared_inter = H, E, cfg.top_k, I, Is
         m.scope = scope if scope else cfg.scope
         m.router = lin(cfg.router_fmt, hw.router, hw.router_s, E, H)
-        m.expert_fmt = cfg.expert_fmt
+        m.expert_fmt = orc_fmt(cfg.expert_fmt)
         self.keep += [hw.gate_up, hw.down]
         m.gate_up = _p(hw.gate_up)
         m.gate_up_scale = _p(sc(hw.gate_up_s)) if hw.gate_up_s is not None else None

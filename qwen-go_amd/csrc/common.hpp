@@ -48,19 +48,19 @@ __device__ __forceinline__ uint32_t lds_offset(const void *p) {
 // 16 * lane (lds_wave_base is wave-uniform).  Issued through asm so that the
 // compiler does not track these loads: the GEMM waits for them explicitly
 // (wait_vm), and loads the compiler does track that were issued later only make
-// its own waits more conservative, never insufficient.
+// its own waits more conservative, never insufficient.  The LDS base goes in
+// through a "{m0}" operand, so the compiler itself writes M0 (and knows its
+// value) before the statement; the s_nop is the wait state between that write
+// and the LDS-direct load that reads it.
 __device__ __forceinline__ void dma16(const void *src, const unsigned char *lds_wave_base) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds_wave_base));
-  // one wait state between the M0 write and the LDS-direct load that reads it
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
 // The same with the nontemporal hint (streamed weights that are read once).
 __device__ __forceinline__ void dma16_nt(const void *src, const unsigned char *lds_wave_base) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds_wave_base));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m0)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
 // 16-byte load with the nontemporal hint.

@@ -44,15 +44,11 @@ __host__ __device__ inline size_t fused_head_bytes(int H, int E) {
 }
 constexpr size_t kLdsLimit = 160 * 1024 - 2048;  // static LDS < 1 KiB
 
-// Longest wait for the other workgroups' router partials, in s_memrealtime
-// ticks (100 MHz): 2 ms.  They normally arrive within a few microseconds; a
-// device that does not run every workgroup of the launch at once would
-// otherwise leave the waiting workgroups spinning.
-constexpr uint64_t kExchangeTicks = 200000;
-
 // Waits until the n tagged words (one per workgroup, saying that its slice of
-// out is zero) carry `tag` (false: timed out).
-__device__ __forceinline__ bool poll_zero_flags(const uint32_t *ztag, int n, uint32_t tag) {
+// out is zero) carry `tag` (false: timed out after `budget` s_memrealtime
+// ticks; a zero budget gives up at once, without polling).
+__device__ __forceinline__ bool poll_zero_flags(const uint32_t *ztag, int n, uint32_t tag, uint64_t budget) {
+  if (budget == 0) return false;
   const int lane = threadIdx.x & 63;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   for (;;) {
@@ -60,16 +56,18 @@ __device__ __forceinline__ bool poll_zero_flags(const uint32_t *ztag, int n, uin
     for (int i = lane; i < n; i += 64)
       mine = mine && __hip_atomic_load(ztag + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
     if (__all(mine)) return true;
-    if (__builtin_amdgcn_s_memrealtime() - t0 > kExchangeTicks) return false;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > budget) return false;
   }
 }
 
 // Polls the 2E tagged router words of this call until every one carries `tag`
-// (or the wait times out: false).  Lane l receives expert l + 64 j in S[j],
-// B[j] (S = -inf, B = 0 past E).
+// (or the wait times out after `budget` ticks, or at once for a zero budget:
+// false).  Lane l receives expert l + 64 j in S[j], B[j] (S = -inf, B = 0
+// past E).
 template <int NJ>
 __device__ __forceinline__ bool poll_router_words(const uint64_t *rtag, int E, uint32_t tag, double (&S)[NJ],
-                                                  double (&B)[NJ]) {
+                                                  double (&B)[NJ], uint64_t budget) {
+  if (budget == 0) return false;
   const int lane = threadIdx.x & 63;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   for (;;) {
@@ -88,7 +86,7 @@ __device__ __forceinline__ bool poll_router_words(const uint64_t *rtag, int E, u
       }
     }
     if (__all(mine)) return true;
-    if (__builtin_amdgcn_s_memrealtime() - t0 > kExchangeTicks) return false;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > budget) return false;
   }
 }
 __host__ inline size_t fused_burst_bytes() { return (size_t)(kData / 64) * kBurstKB * 1024; }
@@ -661,7 +659,7 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
       if (has_routed) {
         gi = writer ? a.ids : nullptr;
         gw = writer ? a.weights : nullptr;
-        if (poll_router_words<NJ>(a.rtag, a.E, a.epoch, S, B)) {
+        if (poll_router_words<NJ>(a.rtag, a.E, a.epoch, S, B, a.xchg_ticks)) {
           rescue = !certified_select_regs<NJ>(S, B, a.E, a.k, a.scope, gi, gw, s_ids, s_w, -2, s_spec, &kth_lo);
         } else {
           // timed out: flag it for the host (the call's result is not
@@ -726,7 +724,7 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   process_rows(te0, te1, 3, use_burst);
   if (ctl && a.fused_router) {
     // out's zeros, every workgroup's slice, before this workgroup's atomics
-    if (poll_zero_flags(a.ztag, gridDim.x, a.epoch)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (poll_zero_flags(a.ztag, gridDim.x, a.epoch, a.xchg_ticks)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     else if (threadIdx.x == 0) __hip_atomic_store(a.xchg_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   if (threadIdx.x == 0) s_exact = need_exact;
@@ -806,6 +804,11 @@ static void fused_launch(const FusedArgs &a0, hipStream_t st) {
   const int blocks = fused_grid(a);
   a.burst = fused_burst_fits(a.H, a.E);
   const size_t lds = fused_lds_bytes(a.H, a.E);
+  if (a.occ_out) {
+    *a.occ_out = 0;
+    (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(a.occ_out, expert_fused_kernel<FMT, ITER, NJ>, kFusedBlock, lds);
+    return;
+  }
   // dynamic LDS above 64 KiB has to be allowed per kernel (once per size)
   static size_t allowed = 64 * 1024;
   if (lds > allowed) {
@@ -846,6 +849,21 @@ static void fused_fmt(const FusedArgs &a, hipStream_t st) {
   case 8: fused_iter<FMT, 8>(a, st); break;
   default: fused_nj<FMT, 0>(a, st); break;
   }
+}
+
+int fused_exchange_blocks(const FusedArgs &a0, int *resident) {
+  FusedArgs a = a0;
+  const int blocks = fused_grid(a);
+  int per_cu = 0;
+  a.occ_out = &per_cu;
+  switch (a.fmt) {
+  case kF32: fused_fmt<kF32>(a, nullptr); break;
+  case kBF16: fused_fmt<kBF16>(a, nullptr); break;
+  case kINT8: fused_fmt<kINT8>(a, nullptr); break;
+  default: fused_fmt<kINT4>(a, nullptr); break;
+  }
+  *resident = per_cu * a.n_cu;
+  return blocks;
 }
 
 bool fused_supported(int fmt, int H, int E) {

@@ -106,16 +106,27 @@ struct FusedArgs {
   // them between its workgroups through rtag (2 words per expert) tagged with
   // epoch (1..255, a new value every call) and zeroes out itself, each
   // workgroup a slice, announced in ztag (one word per workgroup, at most
-  // kMaxExchangeBlocks).  xchg_err (host-visible) is set if an exchange times
-  // out.
+  // kMaxExchangeBlocks).  Every wait for those words gives up after
+  // xchg_ticks s_memrealtime ticks (100 MHz; 0: at once), sets xchg_err
+  // (host-visible) and finishes the workgroup on the exact routing path.
   int fused_router;
   uint64_t *rtag;
   uint32_t *ztag;
   uint32_t epoch;
   int *xchg_err;
+  uint64_t xchg_ticks;
+  int *occ_out;                       // internal: occupancy query instead of a launch
 };
 constexpr int kMaxExchangeBlocks = 4096;
+// Default wait for the exchanged words: 2 ms.  They normally arrive within a
+// few microseconds; a device that does not run every workgroup of the launch
+// at once would otherwise leave the waiting workgroups spinning.
+constexpr uint64_t kExchangeTicks = 200000;
 hipError_t launch_expert_fused(const FusedArgs &a, hipStream_t st);
+// Workgroups of the expert kernel's launch for these arguments, and in
+// *resident how many of its workgroups the device holds at once: the
+// in-kernel router exchange needs every workgroup resident.
+int fused_exchange_blocks(const FusedArgs &a, int *resident);
 bool fused_supported(int fmt, int H, int E);  // the LDS plan fits
 hipError_t launch_zero(float *p, int64_t n, hipStream_t st);
 
@@ -133,8 +144,10 @@ struct PrefillPlan {
 };
 struct PrefillArgs {
   int T, H, E, k, I, Is, Imax;  // Imax = max(I, Is), the row pitch of act
-  int fmt;                      // expert (and shared expert) weight format: BF16, INT8 or INT4
-  int bm;                       // slots per tile, prefill_tile_slots(fmt)
+  int fmt;                      // routed experts' weight format: BF16, INT8 or INT4
+  int bm;                       // slots per routed tile, prefill_tile_slots(fmt)
+  int sfmt;                     // the shared expert's batched format, prefill_shared_fmt
+  int bms;                      // slots per shared tile, prefill_tile_slots(sfmt)
   uint16_t *xb;                 // (T, H) x in bf16
   PrefillPlan p;
   const uint8_t *gu, *dn;       // gate_up (E, 2I, H); down in the reference layout (E, H, I)
@@ -145,7 +158,11 @@ struct PrefillArgs {
   uint16_t *act;                // (slots, Imax) SwiGLU output, bf16
   uint16_t *y;                  // (slots, H) weighted expert outputs, bf16
 };
-bool prefill_supported(int expert_fmt, int shared_fmt, int H, int I, int Is);
+bool prefill_supported(int expert_fmt, int H, int I, int Is);
+// The format the batched path keeps the shared expert in: its own when the
+// GEMMs take it (bf16, int8, int4), else bf16 (an f32 shared expert is
+// rounded to bf16, as the GEMMs round every dequantised weight).
+int prefill_shared_fmt(int shared_fmt);
 int prefill_tile_slots(int expert_fmt);              // slots per GEMM tile for the format
 int prefill_max_tiles(int T, int k, int E, int bm);  // routed tiles, upper bound
 hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, const float *wts, const float *x,
@@ -158,6 +175,13 @@ hipError_t launch_prefill_combine(const PrefillArgs &a, float *out, hipStream_t 
 hipError_t launch_quantize(int bits, const float *w, int64_t n_rows, int cols, uint8_t *codes,
                            uint16_t *scales, hipStream_t st);
 hipError_t launch_dequantize(const DevMat &m, int64_t index, float *out, hipStream_t st);
+// quantLinear.dequantize with f32 scales (rows of cols elements, codes int8 or
+// packed int4) into f32: the storage of the group-32 formats with f32 scales.
+hipError_t launch_dequant_f32s(int bits, const uint8_t *codes, const float *scales, int64_t n_rows, int cols,
+                               float *out, hipStream_t st);
+// f32 -> bf16 (round to nearest even): the batched path's copy of an f32
+// shared expert.
+hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStream_t st);
 // (rows, cols) reference-layout stack -> (cols, rows) transposes, codes and
 // scales moved unchanged (INT4 re-paired along the new rows).
 hipError_t launch_relayout_transpose(int fmt, const uint8_t *src, const uint16_t *ss, int64_t n_mat, int rows,

@@ -35,6 +35,21 @@ struct DevBuf {
   size_t n = 0;
 };
 
+// Device scratch of one forward: router logits / partials, routing, and the
+// batched path's tables and intermediate rows (the handle's workspace, grown
+// with hipMalloc).
+struct Workspace {
+  float *logits = nullptr, *wts = nullptr;
+  double *sb = nullptr;
+  int *fbl = nullptr;      // {count, tokens} for the exact routing path
+  int32_t *ids = nullptr;
+  // batched (MFMA) path buffers
+  uint16_t *xb = nullptr, *act = nullptr;
+  float *sg = nullptr;
+  uint16_t *y = nullptr;
+  PrefillPlan plan{};
+};
+
 }  // namespace
 
 struct qmoe_layer {
@@ -53,23 +68,19 @@ struct qmoe_layer {
   // the batched path (present when it supports the formats)
   DevMat dnr, sdownr;
   bool has_ref_down = false;
+  // the shared expert's gate and up rows for the batched path when they are
+  // kept in another format there (an f32 shared expert: bf16 copies)
+  DevMat sgate_b, sup_b;
+  bool shared_b = false;
   float *shared_gate = nullptr;
   bool has_router = false, has_experts = false, has_shared = false;
 
-  // workspace, sized for ws_T tokens
+  // workspace, sized for ws_T tokens (the batched path's buffers present when ws_mfma)
   int ws_T = 0;
   DevBuf ws;
-  float *logits = nullptr, *wts = nullptr;
+  Workspace w;
   float *xbuf = nullptr, *obuf = nullptr;
-  double *sb = nullptr;
-  int *fbl = nullptr;      // {count, tokens} for the exact routing path
-  int32_t *ids = nullptr;
-  // batched (MFMA) path buffers, present when ws_mfma
   bool ws_mfma = false;
-  uint16_t *xb = nullptr, *act = nullptr;
-  float *sg = nullptr;
-  uint16_t *y = nullptr;
-  PrefillPlan plan{};
   unsigned int *fallbacks = nullptr;  // [0] tokens routed by the exact fallback, [1] certification rescues
   // decode (T = 1): the expert kernel computes the router partials itself and
   // exchanges them between its workgroups as tagged words (2 per expert)
@@ -77,6 +88,8 @@ struct qmoe_layer {
   uint32_t rtag_epoch = 0;            // tag of the last call, 1..255
   int *xchg_err_host = nullptr;       // host-visible flag: an exchange timed out
   int *xchg_err_dev = nullptr;
+  uint64_t xchg_ticks = kExchangeTicks;  // wait budget of the exchange (qmoe_debug_exchange_budget)
+  int xchg_resident = -1;             // the expert kernel's launch fits the device at once (-1: not yet known)
 
   // optional per-stage event timing (qmoe_profile_*)
   uint32_t prof_mask = 0;
@@ -113,7 +126,11 @@ qmoe_status hip_fail(qmoe_layer *l, hipError_t e, const char *what) {
     if (_e != hipSuccess) return hip_fail(l, _e, what); \
   } while (0)
 
-bool valid_fmt(int f) { return f >= QMOE_F32 && f <= QMOE_INT4G32; }
+bool valid_fmt(int f) { return f >= QMOE_F32 && f <= QMOE_INT4G32_F32S; }
+// The group-32 formats with the reference's f32 scales are stored as their
+// exact f32 dequantisation (float32(code) * scale, model/moe.go:134-157).
+bool fmt_f32s(int f) { return f == QMOE_INT8G32_F32S || f == QMOE_INT4G32_F32S; }
+int storage_fmt(int f) { return fmt_f32s(f) ? kF32 : f; }
 
 // Allocates a (n_mat x rows x cols) stack in fmt plus its scales.
 qmoe_status alloc_mat(qmoe_layer *l, DevMat &m, int fmt, int64_t n_mat, int rows, int cols,
@@ -167,17 +184,24 @@ void free_all(qmoe_layer *l) {
 
 // Moves n stored matrices in the reference layout from device staging into
 // m (at matrix index first), transposing when m is stored transposed; a copy
-// in the reference layout also goes into twin, when given.
+// in the reference layout also goes into twin, when given -- in m's format,
+// or, for an f32 m, rounded to bf16 (the batched path's copy of an f32 shared
+// expert).
 qmoe_status place(qmoe_layer *l, const DevMat &m, int64_t first, int64_t n, const uint8_t *src, const uint16_t *ss,
                   const DevMat *twin = nullptr) {
   uint8_t *dst = (uint8_t *)m.w + first * m.mat_bytes;
   uint16_t *ds = m.s ? (uint16_t *)m.s + first * m.mat_scales : nullptr;
-  if (twin) {
+  if (twin && twin->fmt == m.fmt) {
     HIP_TRY(l, hipMemcpyAsync((uint8_t *)twin->w + first * twin->mat_bytes, src, (size_t)(twin->mat_bytes * n),
                               hipMemcpyDeviceToDevice, l->stream), "copy");
     if (twin->s)
       HIP_TRY(l, hipMemcpyAsync((uint16_t *)twin->s + first * twin->mat_scales, ss, (size_t)(twin->mat_scales * n) * 2,
                                 hipMemcpyDeviceToDevice, l->stream), "copy");
+  } else if (twin) {
+    if (m.fmt != kF32 || twin->fmt != kBF16) return fail(l, QMOE_ERR_UNSUPPORTED, "no conversion for this copy");
+    HIP_TRY(l, launch_f32_to_bf16(reinterpret_cast<const float *>(src),
+                                  (uint16_t *)(twin->w + first * twin->mat_bytes), n * m.rows * m.cols, l->stream),
+            "bf16 copy launch");
   }
   if (m.transposed) {
     HIP_TRY(l, launch_relayout_transpose(m.fmt, src, ss, n, m.rows, m.cols, dst, ds, l->stream), "relayout launch");
@@ -190,41 +214,48 @@ qmoe_status place(qmoe_layer *l, const DevMat &m, int64_t first, int64_t n, cons
   return QMOE_OK;
 }
 
-qmoe_status upload(qmoe_layer *l, const DevMat &m, int64_t n_mat, const void *w, const uint16_t *s,
+// Uploads n_mat (rows, cols) matrices given in the ABI format in_fmt into m
+// (and twin, see place): the storage format itself, or a group-32 format with
+// f32 scales, which the device dequantises exactly into m's f32 storage.
+qmoe_status upload(qmoe_layer *l, const DevMat &m, int in_fmt, int64_t n_mat, const void *w, const void *s,
                    const DevMat *twin = nullptr) {
   if (!w) return fail(l, QMOE_ERR_INVALID, "null weight pointer");
-  if (fmt_quant(m.fmt) && !s) return fail(l, QMOE_ERR_INVALID, "null scale pointer for a quantised format");
-  if (m.transposed) {
-    // stage at most ~256 MiB of the reference layout at a time
-    const int64_t per = m.mat_bytes + m.mat_scales * 2;
-    const int64_t chunk = std::min<int64_t>(n_mat, std::max<int64_t>(1, (256ll << 20) / per));
-    uint8_t *tmp = nullptr;
-    HIP_TRY(l, hipMalloc(&tmp, (size_t)(chunk * per)), "hipMalloc upload staging");
-    uint16_t *tsc = m.mat_scales ? (uint16_t *)(tmp + chunk * m.mat_bytes) : nullptr;
-    for (int64_t e0 = 0; e0 < n_mat; e0 += chunk) {
-      const int64_t n = std::min(chunk, n_mat - e0);
-      hipError_t e = hipMemcpy(tmp, (const uint8_t *)w + e0 * m.mat_bytes, (size_t)(n * m.mat_bytes),
-                               hipMemcpyHostToDevice);
-      if (e == hipSuccess && tsc)
-        e = hipMemcpy(tsc, s + e0 * m.mat_scales, (size_t)(n * m.mat_scales) * 2, hipMemcpyHostToDevice);
-      if (e != hipSuccess) {
-        (void)hipFree(tmp);
-        return hip_fail(l, e, "weight upload");
-      }
-      qmoe_status st = place(l, m, e0, n, tmp, tsc, twin);
-      if (st != QMOE_OK) {
-        (void)hipFree(tmp);
-        return st;
-      }
-    }
-    (void)hipFree(tmp);
+  const bool f32s = fmt_f32s(in_fmt);
+  if ((fmt_quant(m.fmt) || f32s) && !s) return fail(l, QMOE_ERR_INVALID, "null scale pointer for a quantised format");
+  if (!m.transposed && !twin && !f32s) {
+    HIP_TRY(l, hipMemcpy((void *)m.w, w, (size_t)(m.mat_bytes * n_mat), hipMemcpyHostToDevice), "weight upload");
+    if (fmt_quant(m.fmt))
+      HIP_TRY(l, hipMemcpy((void *)m.s, s, (size_t)(m.mat_scales * n_mat) * sizeof(uint16_t), hipMemcpyHostToDevice),
+              "scale upload");
     return QMOE_OK;
   }
-  HIP_TRY(l, hipMemcpy((void *)m.w, w, (size_t)(m.mat_bytes * n_mat), hipMemcpyHostToDevice), "weight upload");
-  if (fmt_quant(m.fmt))
-    HIP_TRY(l, hipMemcpy((void *)m.s, s, (size_t)(m.mat_scales * n_mat) * sizeof(uint16_t), hipMemcpyHostToDevice),
-            "scale upload");
-  return QMOE_OK;
+  // staged through the device, at most ~256 MiB of input at a time
+  const int bits = in_fmt == QMOE_INT8G32_F32S ? 8 : 4;
+  const int64_t in_bytes = f32s ? fmt_matrix_bytes(bits == 8 ? kINT8 : kINT4, m.rows, m.cols) : m.mat_bytes;
+  const int64_t in_sc = f32s ? (int64_t)m.rows * (m.cols / kGroup) * 4 : m.mat_scales * 2;
+  const int64_t per = in_bytes + in_sc + (f32s ? m.mat_bytes : 0);
+  const int64_t chunk = std::min<int64_t>(n_mat, std::max<int64_t>(1, (256ll << 20) / per));
+  uint8_t *tmp = nullptr;
+  HIP_TRY(l, hipMalloc(&tmp, (size_t)(chunk * per)), "hipMalloc upload staging");
+  uint8_t *tsc = tmp + chunk * in_bytes;
+  uint8_t *texp = tsc + chunk * in_sc;  // f32 dequantisation (f32s)
+  qmoe_status st = QMOE_OK;
+  for (int64_t e0 = 0; e0 < n_mat && st == QMOE_OK; e0 += chunk) {
+    const int64_t n = std::min(chunk, n_mat - e0);
+    hipError_t e = hipMemcpy(tmp, (const uint8_t *)w + e0 * in_bytes, (size_t)(n * in_bytes), hipMemcpyHostToDevice);
+    if (e == hipSuccess && in_sc)
+      e = hipMemcpy(tsc, (const uint8_t *)s + e0 * in_sc, (size_t)(n * in_sc), hipMemcpyHostToDevice);
+    if (e == hipSuccess && f32s)
+      e = launch_dequant_f32s(bits, tmp, reinterpret_cast<const float *>(tsc), n * m.rows, m.cols,
+                              reinterpret_cast<float *>(texp), l->stream);
+    if (e != hipSuccess) {
+      st = hip_fail(l, e, "weight upload");
+      break;
+    }
+    st = f32s ? place(l, m, e0, n, texp, nullptr, twin) : place(l, m, e0, n, tmp, (const uint16_t *)tsc, twin);
+  }
+  (void)hipFree(tmp);
+  return st;
 }
 
 qmoe_status enter(qmoe_layer *l) {
@@ -264,6 +295,18 @@ hipError_t next_event(qmoe_layer *l, hipEvent_t *ev) {
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// An exchange timeout of the decode kernel leaves the call's output
+// untrustworthy.  The synchronous entry reports it for the call that hit it;
+// an asynchronous call's timeout is reported by the next call on the handle.
+// Either way the flag is cleared once reported.
+qmoe_status take_exchange_error(qmoe_layer *l, const char *which) {
+  if (!*l->xchg_err_host) return QMOE_OK;
+  *l->xchg_err_host = 0;
+  return fail(l, QMOE_ERR_HIP, std::string(which) +
+                                   ": the decode kernel's workgroups timed out exchanging router partials (not all "
+                                   "of them ran at once); that call's output and routing are not valid");
+}
+
 // Token counts above this run the batched MFMA path when its formats allow.
 constexpr int kMaxGemvTokens = 32;
 // Tokens x experts from which the batched routing uses the matrix-core
@@ -272,8 +315,7 @@ constexpr int64_t kCertManyMin = (int64_t)1 << 20;
 
 bool use_mfma(const qmoe_layer *l, int T) {
   const qmoe_desc &d = l->d;
-  return T > kMaxGemvTokens && l->has_ref_down &&
-         prefill_supported(d.expert_fmt, d.shared_fmt, d.hidden, d.moe_inter, d.shared_inter);
+  return T > kMaxGemvTokens && l->has_ref_down && prefill_supported(l->gu.fmt, d.hidden, d.moe_inter, d.shared_inter);
 }
 
 qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
@@ -292,8 +334,9 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_fbl = take((size_t)(nT + 1) * 4);      // tokens queued for the exact routing path
   const bool want_mfma = mfma || l->ws_mfma;
   const size_t pairs = (size_t)nT * d.top_k, slots = pairs + (size_t)nT;
-  const int bm = prefill_tile_slots(d.expert_fmt);
-  const size_t tiles = (size_t)prefill_max_tiles(nT, d.top_k, d.n_experts, bm) + (nT + bm - 1) / bm;
+  const int bm = prefill_tile_slots(l->gu.fmt);
+  const int bms = d.shared_inter > 0 ? prefill_tile_slots(l->sdownr.fmt) : bm;
+  const size_t tiles = (size_t)prefill_max_tiles(nT, d.top_k, d.n_experts, bm) + (nT + bms - 1) / bms;
   const int imax = std::max(d.moe_inter, d.shared_inter);
   size_t o_xb = 0, o_sg = 0, o_tok = 0, o_wsl = 0, o_slot = 0, o_goff = 0, o_gcnt = 0, o_cur = 0, o_tg = 0, o_tm = 0,
          o_nt = 0, o_act = 0, o_y = 0;
@@ -325,40 +368,51 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   }
   l->ws.n = off;
   char *b = (char *)l->ws.p;
-  l->logits = (float *)(b + o_logits);
-  l->ids = (int32_t *)(b + o_ids);
-  l->wts = (float *)(b + o_wts);
+  Workspace &w = l->w;
+  w = Workspace{};
+  w.logits = (float *)(b + o_logits);
+  w.ids = (int32_t *)(b + o_ids);
+  w.wts = (float *)(b + o_wts);
   l->xbuf = (float *)(b + o_x);
   l->obuf = (float *)(b + o_o);
-  l->sb = (double *)(b + o_sb);
-  l->fbl = (int *)(b + o_fbl);
+  w.sb = (double *)(b + o_sb);
+  w.fbl = (int *)(b + o_fbl);
   l->ws_mfma = want_mfma;
   if (want_mfma) {
-    l->xb = (uint16_t *)(b + o_xb);
-    l->sg = (float *)(b + o_sg);
-    l->plan.tok = (int32_t *)(b + o_tok);
-    l->plan.wslot = (float *)(b + o_wsl);
-    l->plan.slot_of = (int32_t *)(b + o_slot);
-    l->plan.grp_off = (int32_t *)(b + o_goff);
-    l->plan.grp_cnt = (int32_t *)(b + o_gcnt);
-    l->plan.cursor = (int32_t *)(b + o_cur);
-    l->plan.tile_grp = (int32_t *)(b + o_tg);
-    l->plan.tile_m0 = (int32_t *)(b + o_tm);
-    l->plan.n_tiles = (int32_t *)(b + o_nt);
-    l->act = (uint16_t *)(b + o_act);
-    l->y = (uint16_t *)(b + o_y);
+    w.xb = (uint16_t *)(b + o_xb);
+    w.sg = (float *)(b + o_sg);
+    w.plan.tok = (int32_t *)(b + o_tok);
+    w.plan.wslot = (float *)(b + o_wsl);
+    w.plan.slot_of = (int32_t *)(b + o_slot);
+    w.plan.grp_off = (int32_t *)(b + o_goff);
+    w.plan.grp_cnt = (int32_t *)(b + o_gcnt);
+    w.plan.cursor = (int32_t *)(b + o_cur);
+    w.plan.tile_grp = (int32_t *)(b + o_tg);
+    w.plan.tile_m0 = (int32_t *)(b + o_tm);
+    w.plan.n_tiles = (int32_t *)(b + o_nt);
+    w.act = (uint16_t *)(b + o_act);
+    w.y = (uint16_t *)(b + o_y);
   }
   l->ws_T = nT;
   return QMOE_OK;
 }
 
-qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, int32_t *d_ids,
-                        float *d_w, hipStream_t st) {
+// The kernels of one forward of T tokens on stream st, with scratch from ws.
+// profile = false records no events.
+qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, int T, float *d_out, int32_t *d_ids,
+                        float *d_w, hipStream_t st, bool profile = true) {
   const qmoe_desc &d = l->d;
   if (!l->has_router || !l->has_experts || (d.shared_inter > 0 && !l->has_shared))
     return fail(l, QMOE_ERR_STATE, "weights not uploaded (router, experts and shared expert are required)");
-  int32_t *ids = d_ids ? d_ids : l->ids;
-  float *wts = d_w ? d_w : l->wts;
+  int32_t *ids = d_ids ? d_ids : ws.ids;
+  float *wts = d_w ? d_w : ws.wts;
+  const uint32_t prof_mask_saved = l->prof_mask;
+  if (!profile) l->prof_mask = 0;
+  struct Restore {
+    qmoe_layer *l;
+    uint32_t m;
+    ~Restore() { l->prof_mask = m; }
+  } restore{l, prof_mask_saved};
   const int H = d.hidden, E = d.n_experts, k = d.top_k, I = d.moe_inter, Is = d.shared_inter;
 
   // routing for T > 32.  Many tokens x experts with a bf16 router: bounded
@@ -367,15 +421,15 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   // and the exact softmax and selection.
   auto route_many = [&]() -> qmoe_status {
     if ((int64_t)T * E >= kCertManyMin && router_cert_mfma_supported(l->router)) {
-      STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, l->sb, st),
+      STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, ws.sb, st),
             "router partials launch");
       STAGE(l, QMOE_STAGE_SELECT, st,
-            launch_select_candidates(d_x, T, l->router, k, l->scope, l->sb, ids, wts, l->fbl, l->fallbacks, st),
+            launch_select_candidates(d_x, T, l->router, k, l->scope, ws.sb, ids, wts, ws.fbl, l->fallbacks, st),
             "candidate selection launch");
       return QMOE_OK;
     }
-    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, l->logits, st), "router logits launch");
-    STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(l->logits, T, E, k, l->scope, ids, wts, st),
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, ws.logits, st), "router logits launch");
+    STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(ws.logits, T, E, k, l->scope, ids, wts, st),
           "softmax/select launch");
     return QMOE_OK;
   };
@@ -391,10 +445,12 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
     pa.I = I;
     pa.Is = Is;
     pa.Imax = std::max(I, Is);
-    pa.fmt = d.expert_fmt;
-    pa.bm = prefill_tile_slots(d.expert_fmt);
-    pa.xb = l->xb;
-    pa.p = l->plan;
+    pa.fmt = l->gu.fmt;
+    pa.bm = prefill_tile_slots(l->gu.fmt);
+    pa.sfmt = Is > 0 ? l->sdownr.fmt : pa.fmt;
+    pa.bms = prefill_tile_slots(pa.sfmt);
+    pa.xb = ws.xb;
+    pa.p = ws.plan;
     pa.gu = l->gu.w;
     pa.dn = l->dnr.w;
     pa.gu_s = l->gu.s;
@@ -404,16 +460,17 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
     pa.dn_bytes = l->dnr.mat_bytes;
     pa.dn_scales = l->dnr.mat_scales;
     if (Is > 0) {
-      pa.sgate = l->sgate.w;
-      pa.sup = l->sup.w;
+      const DevMat &bg = l->shared_b ? l->sgate_b : l->sgate, &bu = l->shared_b ? l->sup_b : l->sup;
+      pa.sgate = bg.w;
+      pa.sup = bu.w;
       pa.sdown = l->sdownr.w;
-      pa.sgate_s = l->sgate.s;
-      pa.sup_s = l->sup.s;
+      pa.sgate_s = bg.s;
+      pa.sup_s = bu.s;
       pa.sdown_s = l->sdownr.s;
     }
-    pa.act = l->act;
-    pa.y = l->y;
-    STAGE(l, QMOE_STAGE_DISPATCH, st, launch_prefill_dispatch(pa, ids, wts, d_x, l->shared_gate, l->sg, st),
+    pa.act = ws.act;
+    pa.y = ws.y;
+    STAGE(l, QMOE_STAGE_DISPATCH, st, launch_prefill_dispatch(pa, ids, wts, d_x, l->shared_gate, ws.sg, st),
           "dispatch launch");
     STAGE(l, QMOE_STAGE_GATE_UP, st, launch_prefill_gate_up(pa, false, st), "gate_up launch");
     if (Is > 0)
@@ -426,17 +483,33 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
 
   // T = 1 with a bf16 router of at most 4 chunks per lane: the expert kernel
   // computes the router partials itself (no router launch) and zeroes out.
+  // Its workgroups exchange those partials, so every one of them must be
+  // resident at once (checked once per handle with the occupancy calculator).
   const int rcpl = (H / 8 + 63) / 64;
-  const bool fused_router = T == 1 && l->router.fmt == kBF16 && H % 8 == 0 && (rcpl == 1 || rcpl == 2 || rcpl == 4) &&
-                            E <= 7 * l->n_cu && fused_supported(l->gu.fmt, H, E);
-  if (fused_router && *l->xchg_err_host)
-    return fail(l, QMOE_ERR_HIP, "an earlier decode call timed out exchanging router partials between workgroups "
-                                 "(the device did not run all of its workgroups at once)");
+  bool fused_router = T == 1 && l->router.fmt == kBF16 && H % 8 == 0 && (rcpl == 1 || rcpl == 2 || rcpl == 4) &&
+                      E <= 7 * l->n_cu && fused_supported(l->gu.fmt, H, E);
+  if (fused_router && l->xchg_resident < 0) {
+    FusedArgs q{};
+    q.T = 1;
+    q.H = H;
+    q.E = E;
+    q.I = I;
+    q.Is = Is;
+    q.fmt = l->gu.fmt;
+    q.k_routed = k;
+    q.with_shared = Is > 0 && l->sgate.fmt == l->gu.fmt;
+    q.n_cu = l->n_cu;
+    int resident = 0;
+    const int blocks = fused_exchange_blocks(q, &resident);
+    (void)hipGetLastError();
+    l->xchg_resident = blocks <= resident && blocks <= kMaxExchangeBlocks && E <= 7 * blocks ? 1 : 0;
+  }
+  fused_router = fused_router && l->xchg_resident == 1;
   const bool cert = !fused_router && T <= kMaxGemvTokens && router_certified_supported(l->router);
   if (fused_router) {
     // nothing to launch before the expert kernel
   } else if (cert) {
-    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, l->sb, d_out, st), "router launch");
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, ws.sb, d_out, st), "router launch");
   } else {
     if (qmoe_status rs = route_many()) return rs;
     HIP_TRY(l, launch_zero(d_out, (int64_t)T * H, st), "zero launch");
@@ -453,7 +526,7 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
   f.rw = l->router.w;
   f.rs = l->router.s;
   f.rfmt = l->router.fmt;
-  f.sb = cert ? l->sb : nullptr;
+  f.sb = cert ? ws.sb : nullptr;
   f.fmt = l->gu.fmt;
   f.gu = l->gu.w;
   f.gu_s = l->gu.s;
@@ -482,15 +555,16 @@ qmoe_status run_forward(qmoe_layer *l, const float *d_x, int T, float *d_out, in
     f.ztag = reinterpret_cast<uint32_t *>(l->rtag + 2 * (size_t)E);
     f.epoch = l->rtag_epoch;
     f.xchg_err = l->xchg_err_dev;
+    f.xchg_ticks = l->xchg_ticks;
   }
   f.out = d_out;
   f.k_routed = k;
-  f.with_shared = Is > 0 && d.shared_fmt == d.expert_fmt;
+  f.with_shared = Is > 0 && l->sgate.fmt == l->gu.fmt;
   f.n_cu = l->n_cu;
   STAGE(l, QMOE_STAGE_FUSED, st, launch_expert_fused(f, st), "fused expert launch");
-  if (Is > 0 && d.shared_fmt != d.expert_fmt) {
+  if (Is > 0 && l->sgate.fmt != l->gu.fmt) {
     // shared expert in its own format: a second launch of the same kernel
-    f.fmt = d.shared_fmt;
+    f.fmt = l->sgate.fmt;
     f.k_routed = 0;
     f.with_shared = 1;
     f.fused_router = 0;
@@ -537,8 +611,8 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
     return fail(nullptr, QMOE_ERR_UNSUPPORTED, "n_experts > 1024 or top_k > 64");
   if (d.hidden > 16384)
     return fail(nullptr, QMOE_ERR_UNSUPPORTED, "hidden > 16384");
-  if (!fused_supported(d.expert_fmt, d.hidden, d.n_experts) ||
-      (d.shared_inter > 0 && !fused_supported(d.shared_fmt, d.hidden, d.n_experts)))
+  if (!fused_supported(storage_fmt(d.expert_fmt), d.hidden, d.n_experts) ||
+      (d.shared_inter > 0 && !fused_supported(storage_fmt(d.shared_fmt), d.hidden, d.n_experts)))
     return fail(nullptr, QMOE_ERR_UNSUPPORTED, "hidden too large for the expert kernel's LDS plan");
   int ndev = 0;
   hipError_t e = hipGetDeviceCount(&ndev);
@@ -562,20 +636,27 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
   }
   qmoe_status s;
   const int H = d.hidden, E = d.n_experts, I = d.moe_inter, Is = d.shared_inter;
-  if ((s = alloc_mat(l, l->router, d.router_fmt, 1, E, H)) != QMOE_OK ||
-      (s = alloc_mat(l, l->gu, d.expert_fmt, E, 2 * I, H)) != QMOE_OK ||
-      (s = alloc_mat(l, l->dn, d.expert_fmt, E, H, I, true)) != QMOE_OK ||
-      (Is > 0 && ((s = alloc_mat(l, l->sgate, d.shared_fmt, 1, Is, H)) != QMOE_OK ||
-                  (s = alloc_mat(l, l->sup, d.shared_fmt, 1, Is, H)) != QMOE_OK ||
-                  (s = alloc_mat(l, l->sdown, d.shared_fmt, 1, H, Is, true)) != QMOE_OK))) {
+  const int rf = storage_fmt(d.router_fmt), ef = storage_fmt(d.expert_fmt), sf = storage_fmt(d.shared_fmt);
+  if ((s = alloc_mat(l, l->router, rf, 1, E, H)) != QMOE_OK ||
+      (s = alloc_mat(l, l->gu, ef, E, 2 * I, H)) != QMOE_OK ||
+      (s = alloc_mat(l, l->dn, ef, E, H, I, true)) != QMOE_OK ||
+      (Is > 0 && ((s = alloc_mat(l, l->sgate, sf, 1, Is, H)) != QMOE_OK ||
+                  (s = alloc_mat(l, l->sup, sf, 1, Is, H)) != QMOE_OK ||
+                  (s = alloc_mat(l, l->sdown, sf, 1, H, Is, true)) != QMOE_OK))) {
     g_create_error = l->err;
     free_all(l);
     delete l;
     return s;
   }
-  l->has_ref_down = prefill_supported(d.expert_fmt, d.shared_fmt, H, I, Is);
-  if (l->has_ref_down && ((s = alloc_mat(l, l->dnr, d.expert_fmt, E, H, I)) != QMOE_OK ||
-                          (Is > 0 && (s = alloc_mat(l, l->sdownr, d.shared_fmt, 1, H, Is)) != QMOE_OK))) {
+  // the batched path: experts' down in the reference layout; the shared
+  // expert in the format its GEMMs take (bf16 copies of an f32 one)
+  l->has_ref_down = prefill_supported(ef, H, I, Is);
+  const int sbf = prefill_shared_fmt(sf);
+  l->shared_b = l->has_ref_down && Is > 0 && sbf != sf;
+  if (l->has_ref_down && ((s = alloc_mat(l, l->dnr, ef, E, H, I)) != QMOE_OK ||
+                          (Is > 0 && (s = alloc_mat(l, l->sdownr, sbf, 1, H, Is)) != QMOE_OK) ||
+                          (l->shared_b && ((s = alloc_mat(l, l->sgate_b, sbf, 1, Is, H)) != QMOE_OK ||
+                                           (s = alloc_mat(l, l->sup_b, sbf, 1, Is, H)) != QMOE_OK)))) {
     g_create_error = l->err;
     free_all(l);
     delete l;
@@ -647,31 +728,32 @@ void qmoe_destroy(qmoe_layer *layer) {
   delete layer;
 }
 
-qmoe_status qmoe_set_router(qmoe_layer *l, const void *w, const uint16_t *scales) {
+qmoe_status qmoe_set_router(qmoe_layer *l, const void *w, const void *scales) {
   if (!l) return QMOE_ERR_INVALID;
   std::lock_guard<std::mutex> g(l->mu);
   qmoe_status s = enter(l);
   if (s) return s;
-  if ((s = upload(l, l->router, 1, w, scales)) != QMOE_OK) return s;
+  if ((s = upload(l, l->router, l->d.router_fmt, 1, w, scales)) != QMOE_OK) return s;
   l->has_router = true;
   return QMOE_OK;
 }
 
-qmoe_status qmoe_set_experts(qmoe_layer *l, const void *gate_up, const uint16_t *gate_up_scales,
-                             const void *down, const uint16_t *down_scales) {
+qmoe_status qmoe_set_experts(qmoe_layer *l, const void *gate_up, const void *gate_up_scales, const void *down,
+                             const void *down_scales) {
   if (!l) return QMOE_ERR_INVALID;
   std::lock_guard<std::mutex> g(l->mu);
   qmoe_status s = enter(l);
   if (s) return s;
   const int E = l->d.n_experts;
-  if ((s = upload(l, l->gu, E, gate_up, gate_up_scales)) != QMOE_OK) return s;
-  if ((s = upload(l, l->dn, E, down, down_scales, l->has_ref_down ? &l->dnr : nullptr)) != QMOE_OK) return s;
+  const int f = l->d.expert_fmt;
+  if ((s = upload(l, l->gu, f, E, gate_up, gate_up_scales)) != QMOE_OK) return s;
+  if ((s = upload(l, l->dn, f, E, down, down_scales, l->has_ref_down ? &l->dnr : nullptr)) != QMOE_OK) return s;
   l->has_experts = true;
   return QMOE_OK;
 }
 
-qmoe_status qmoe_set_shared(qmoe_layer *l, const void *gate, const uint16_t *gate_scales, const void *up,
-                            const uint16_t *up_scales, const void *down, const uint16_t *down_scales,
+qmoe_status qmoe_set_shared(qmoe_layer *l, const void *gate, const void *gate_scales, const void *up,
+                            const void *up_scales, const void *down, const void *down_scales,
                             const float *shared_gate) {
   if (!l) return QMOE_ERR_INVALID;
   std::lock_guard<std::mutex> g(l->mu);
@@ -679,9 +761,10 @@ qmoe_status qmoe_set_shared(qmoe_layer *l, const void *gate, const uint16_t *gat
   if (s) return s;
   if (l->d.shared_inter <= 0) return fail(l, QMOE_ERR_STATE, "layer has no shared expert (shared_inter == 0)");
   if (!shared_gate) return fail(l, QMOE_ERR_INVALID, "null shared_gate");
-  if ((s = upload(l, l->sgate, 1, gate, gate_scales)) != QMOE_OK) return s;
-  if ((s = upload(l, l->sup, 1, up, up_scales)) != QMOE_OK) return s;
-  if ((s = upload(l, l->sdown, 1, down, down_scales, l->has_ref_down ? &l->sdownr : nullptr)) != QMOE_OK) return s;
+  const int f = l->d.shared_fmt;
+  if ((s = upload(l, l->sgate, f, 1, gate, gate_scales, l->shared_b ? &l->sgate_b : nullptr)) != QMOE_OK) return s;
+  if ((s = upload(l, l->sup, f, 1, up, up_scales, l->shared_b ? &l->sup_b : nullptr)) != QMOE_OK) return s;
+  if ((s = upload(l, l->sdown, f, 1, down, down_scales, l->has_ref_down ? &l->sdownr : nullptr)) != QMOE_OK) return s;
   HIP_TRY(l, hipMemcpy(l->shared_gate, shared_gate, (size_t)l->d.hidden * 4, hipMemcpyHostToDevice),
           "shared gate upload");
   l->has_shared = true;
@@ -740,6 +823,14 @@ qmoe_status qmoe_quantize_experts(qmoe_layer *l, const float *gate_up, const flo
   return QMOE_OK;
 }
 
+// Tokens per launch sequence: the batched path's slot tables hold at most
+// 65535 (token, rank) pairs, so longer batches run in chunks (each output row
+// depends only on its own token, so chunking changes no result).
+int chunk_tokens(const qmoe_layer *l) {
+  const int c = 65535 / l->d.top_k;
+  return c >= 256 ? c / 64 * 64 : c;
+}
+
 qmoe_status qmoe_forward_device(qmoe_layer *l, const float *d_x, int32_t T, float *d_out, int32_t *d_ids,
                                 float *d_weights, void *stream) {
   if (!l) return QMOE_ERR_INVALID;
@@ -749,10 +840,19 @@ qmoe_status qmoe_forward_device(qmoe_layer *l, const float *d_x, int32_t T, floa
   if (T < 0) return fail(l, QMOE_ERR_INVALID, "T < 0");
   if (T == 0) return QMOE_OK;
   if (!d_x || !d_out) return fail(l, QMOE_ERR_INVALID, "null x or out pointer");
-  if ((int64_t)T * l->d.top_k > 65535) return fail(l, QMOE_ERR_UNSUPPORTED, "T * top_k > 65535");
+  if ((s = take_exchange_error(l, "an earlier asynchronous forward")) != QMOE_OK) return s;
   hipStream_t st = (hipStream_t)stream;
-  if ((s = ensure_workspace(l, T, st)) != QMOE_OK) return s;
-  return run_forward(l, d_x, T, d_out, d_ids, d_weights, st);
+  const int tc = chunk_tokens(l);
+  const int H = l->d.hidden, k = l->d.top_k;
+  if ((s = ensure_workspace(l, std::min(T, tc), st)) != QMOE_OK) return s;
+  for (int t0 = 0; t0 < T; t0 += tc) {
+    const int n = std::min(tc, T - t0);
+    if ((s = run_forward(l, l->w, d_x + (size_t)t0 * H, n, d_out + (size_t)t0 * H,
+                         d_ids ? d_ids + (size_t)t0 * k : nullptr,
+                         d_weights ? d_weights + (size_t)t0 * k : nullptr, st)) != QMOE_OK)
+      return s;
+  }
+  return QMOE_OK;
 }
 
 qmoe_status qmoe_forward(qmoe_layer *l, const float *x, int32_t T, float *out, int32_t *ids, float *weights) {
@@ -763,17 +863,25 @@ qmoe_status qmoe_forward(qmoe_layer *l, const float *x, int32_t T, float *out, i
   if (T < 0) return fail(l, QMOE_ERR_INVALID, "T < 0");
   if (T == 0) return QMOE_OK;
   if (!x || !out) return fail(l, QMOE_ERR_INVALID, "null x or out pointer");
-  if ((int64_t)T * l->d.top_k > 65535) return fail(l, QMOE_ERR_UNSUPPORTED, "T * top_k > 65535");
-  if ((s = ensure_workspace(l, T, nullptr)) != QMOE_OK) return s;
-  const size_t xb = (size_t)T * l->d.hidden * 4;
-  HIP_TRY(l, hipMemcpyAsync(l->xbuf, x, xb, hipMemcpyHostToDevice, l->stream), "x upload");
-  if ((s = run_forward(l, l->xbuf, T, l->obuf, l->ids, l->wts, l->stream)) != QMOE_OK) return s;
-  HIP_TRY(l, hipMemcpyAsync(out, l->obuf, xb, hipMemcpyDeviceToHost, l->stream), "out download");
-  const size_t kb = (size_t)T * l->d.top_k * 4;
-  if (ids) HIP_TRY(l, hipMemcpyAsync(ids, l->ids, kb, hipMemcpyDeviceToHost, l->stream), "ids download");
-  if (weights) HIP_TRY(l, hipMemcpyAsync(weights, l->wts, kb, hipMemcpyDeviceToHost, l->stream), "weights download");
-  HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
-  return QMOE_OK;
+  if ((s = take_exchange_error(l, "an earlier asynchronous forward")) != QMOE_OK) return s;
+  const int tc = chunk_tokens(l);
+  const int H = l->d.hidden, k = l->d.top_k;
+  if ((s = ensure_workspace(l, std::min(T, tc), nullptr)) != QMOE_OK) return s;
+  for (int t0 = 0; t0 < T; t0 += tc) {
+    const int n = std::min(tc, T - t0);
+    const size_t xb = (size_t)n * H * 4, kb = (size_t)n * k * 4;
+    HIP_TRY(l, hipMemcpyAsync(l->xbuf, x + (size_t)t0 * H, xb, hipMemcpyHostToDevice, l->stream), "x upload");
+    if ((s = run_forward(l, l->w, l->xbuf, n, l->obuf, l->w.ids, l->w.wts, l->stream)) != QMOE_OK) return s;
+    HIP_TRY(l, hipMemcpyAsync(out + (size_t)t0 * H, l->obuf, xb, hipMemcpyDeviceToHost, l->stream), "out download");
+    if (ids)
+      HIP_TRY(l, hipMemcpyAsync(ids + (size_t)t0 * k, l->w.ids, kb, hipMemcpyDeviceToHost, l->stream), "ids download");
+    if (weights)
+      HIP_TRY(l, hipMemcpyAsync(weights + (size_t)t0 * k, l->w.wts, kb, hipMemcpyDeviceToHost, l->stream),
+              "weights download");
+    // the next chunk reuses the staging buffers
+    HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+  }
+  return take_exchange_error(l, "this forward");
 }
 
 qmoe_status qmoe_dequant_debug(qmoe_layer *l, int32_t which, int32_t expert, float *out) {
@@ -821,9 +929,9 @@ qmoe_status qmoe_router_bounds_debug(qmoe_layer *l, const float *x, int32_t T, d
   const size_t nx = (size_t)T * l->d.hidden, nsb = (size_t)T * l->d.n_experts * 2;
   hipError_t e = hipMemcpyAsync(l->xbuf, x, nx * 4, hipMemcpyHostToDevice, l->stream);
   if (e == hipSuccess)
-    e = small ? launch_router_sb(l->xbuf, T, l->router, l->sb, nullptr, l->stream)
-              : launch_router_cert_mfma(l->xbuf, T, l->router, l->sb, l->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(sb_out, l->sb, nsb * 8, hipMemcpyDeviceToHost, l->stream);
+    e = small ? launch_router_sb(l->xbuf, T, l->router, l->w.sb, nullptr, l->stream)
+              : launch_router_cert_mfma(l->xbuf, T, l->router, l->w.sb, l->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(sb_out, l->w.sb, nsb * 8, hipMemcpyDeviceToHost, l->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
   if (e != hipSuccess) return hip_fail(l, e, "router_bounds_debug");
   return QMOE_OK;
@@ -890,6 +998,15 @@ qmoe_status qmoe_router_rescues(qmoe_layer *l, int64_t *count) {
 int32_t qmoe_forward_path(const qmoe_layer *l, int32_t T) {
   if (!l) return -1;
   return use_mfma(l, T) ? QMOE_PATH_MFMA : QMOE_PATH_GEMV;
+}
+
+qmoe_status qmoe_debug_exchange_budget(qmoe_layer *l, int64_t ticks) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  l->xchg_ticks = ticks < 0 ? kExchangeTicks : (uint64_t)ticks;
+  return QMOE_OK;
 }
 
 int64_t qmoe_device_bytes(const qmoe_layer *l) {

@@ -95,7 +95,8 @@ constexpr int kDispatchThreads = 1024;
 // cursors that scatter_kernel advances.
 template <int J>
 __global__ void __launch_bounds__(kDispatchThreads)
-    dispatch_kernel(const int32_t *__restrict__ ids, int T, int k, int E, int with_shared, int bm, PrefillPlan p) {
+    dispatch_kernel(const int32_t *__restrict__ ids, int T, int k, int E, int with_shared, int bm, int bms,
+                    PrefillPlan p) {
   __shared__ int cnt[1024], incl[1024], tincl[1024];
   const int tid = threadIdx.x;
   const int n = T * k;
@@ -143,10 +144,11 @@ __global__ void __launch_bounds__(kDispatchThreads)
       p.tile_m0[toff + q] = q * bm;
     }
   }
-  const int shared_tiles = with_shared ? (T + bm - 1) / bm : 0;
+  // the shared expert's tiles hold bms slots (its GEMMs may run another format)
+  const int shared_tiles = with_shared ? (T + bms - 1) / bms : 0;
   for (int q = tid; q < shared_tiles; q += kDispatchThreads) {
     p.tile_grp[routed_tiles + q] = E;
-    p.tile_m0[routed_tiles + q] = q * bm;
+    p.tile_m0[routed_tiles + q] = q * bms;
   }
   if (tid == 0) {
     p.n_tiles[0] = routed_tiles;
@@ -353,8 +355,7 @@ __device__ __forceinline__ void dequant_piece(const uint4 v, float s, uint32_t (
 // 4 bytes per lane from global memory into LDS at lds_wave_base + 4 * lane.
 __device__ __forceinline__ void dma4(const void *src, const unsigned char *lds_wave_base) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds_wave_base));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
 // Work order, XCD-aware: workgroups are dealt to the 8 XCDs round-robin by
@@ -660,12 +661,16 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t *__restrict
 
 // ------------------------------------------------------------- launchers
 
-bool prefill_supported(int expert_fmt, int shared_fmt, int H, int I, int Is) {
-  // bf16, int8 or int4 experts; the shared expert (if any) in the same format;
-  // whole column chunks (gate_up: 128 intermediate columns, down: 256 outputs)
+bool prefill_supported(int expert_fmt, int H, int I, int Is) {
+  // bf16, int8 or int4 experts (the shared expert in any format: see
+  // prefill_shared_fmt); whole column chunks (gate_up: 128 intermediate
+  // columns, down: 256 outputs)
   if (expert_fmt != kBF16 && expert_fmt != kINT8 && expert_fmt != kINT4) return false;
-  if (Is > 0 && shared_fmt != expert_fmt) return false;
   return H % kBN == 0 && I % (kBN / 2) == 0 && (Is == 0 || Is % (kBN / 2) == 0);
+}
+
+int prefill_shared_fmt(int shared_fmt) {
+  return shared_fmt == kBF16 || shared_fmt == kINT8 || shared_fmt == kINT4 ? shared_fmt : kBF16;
 }
 
 int prefill_tile_slots(int expert_fmt) {
@@ -688,7 +693,7 @@ hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, con
                      sg);
   const int n = a.T * a.k;
 #define L(J) QMOE_LAUNCH(dispatch_kernel<J>, dim3(1), dim3(kDispatchThreads), 0, st, ids, a.T, a.k, a.E, \
-                         (int)with_shared, a.bm, a.p)
+                         (int)with_shared, a.bm, a.bms, a.p)
   if (n <= 4 * kDispatchThreads) L(4);
   else if (n <= 16 * kDispatchThreads) L(16);
   else if (n <= 48 * kDispatchThreads) L(48);
@@ -701,11 +706,13 @@ hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, con
 
 template <int KIND>
 static hipError_t gemm_launch(const PrefillArgs &a, bool shared, int ny, hipStream_t st) {
-  const int tiles = shared ? (a.T + a.bm - 1) / a.bm : prefill_max_tiles(a.T, a.k, a.E, a.bm);
+  // the shared expert's GEMMs run in its own format, on tiles of its own size
+  const int fmt = shared ? a.sfmt : a.fmt, bm = shared ? a.bms : a.bm;
+  const int tiles = shared ? (a.T + bm - 1) / bm : prefill_max_tiles(a.T, a.k, a.E, bm);
   const int blocks = (tiles + kXcds - 1) / kXcds * kXcds * ny;
-  if (a.bm != prefill_tile_slots(a.fmt)) return hipErrorInvalidValue;
+  if (bm != prefill_tile_slots(fmt)) return hipErrorInvalidValue;
 #define L(BF) QMOE_LAUNCH((grouped_gemm<KIND, BF>), dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny)
-  switch (a.fmt) {
+  switch (fmt) {
   case kBF16: L(kBF16); break;
   case kINT8: L(kINT8); break;
   case kINT4: L(kINT4); break;

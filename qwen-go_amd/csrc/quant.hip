@@ -158,6 +158,62 @@ hipError_t launch_dequantize(const DevMat &m, int64_t index, float *out, hipStre
   return hipGetLastError();
 }
 
+// quantLinear.dequantize (model/moe.go:134-157) with the reference's own f32
+// scales (qwen-quant writes them as F32, cmd/qwen-quant/main.go:207-210):
+// n_rows rows of cols elements, w = float32(code) * scale, one f32 multiply
+// per element; int4: byte c of a row holds element 2c in its high nibble and
+// 2c+1 in its low nibble, value = float32(nibble) - 8.
+template <int BITS>
+__global__ void __launch_bounds__(256) dequant_f32s_kernel(const uint8_t *__restrict__ codes,
+                                                           const float *__restrict__ scales, int64_t n_rows, int cols,
+                                                           float *__restrict__ out) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_rows * cols) return;
+  const int64_t o = i / cols;
+  const int c = (int)(i % cols);
+  const float sc = scales[o * (cols / kGroup) + c / kGroup];
+  float v;
+  if constexpr (BITS == 8) {
+    v = (float)(int8_t)codes[i];
+  } else {
+    const uint8_t b = codes[o * (cols / 2) + c / 2];
+    v = (float)((c % 2 == 0) ? (b >> 4) : (b & 0xf)) - 8.0f;
+  }
+  out[i] = v * sc;
+}
+
+hipError_t launch_dequant_f32s(int bits, const uint8_t *codes, const float *scales, int64_t n_rows, int cols,
+                               float *out, hipStream_t st) {
+  const int64_t n = n_rows * cols;
+  if (n <= 0) return hipSuccess;
+  dim3 grid((unsigned)((n + 255) / 256));
+  if (bits == 8)
+    hipLaunchKernelGGL(dequant_f32s_kernel<8>, grid, dim3(256), 0, st, codes, scales, n_rows, cols, out);
+  else
+    hipLaunchKernelGGL(dequant_f32s_kernel<4>, grid, dim3(256), 0, st, codes, scales, n_rows, cols, out);
+  return hipGetLastError();
+}
+
+// f32 -> bf16 bit patterns, round to nearest even (NaNs stay quiet NaNs).
+__global__ void __launch_bounds__(256) f32_to_bf16_kernel(const float *__restrict__ src, uint16_t *__restrict__ dst,
+                                                          int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t u = __float_as_uint(src[i]);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) {
+    dst[i] = (uint16_t)((u >> 16) | 0x40u);
+    return;
+  }
+  dst[i] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, dst, n);
+  return hipGetLastError();
+}
+
 // Re-layout of n_mat stored (rows, cols) matrices in the reference layout into
 // their (cols, rows) transposes, keeping every stored code and scale: the
 // element (o, c) moves to (c, o); INT4 nibbles pair up along the new rows

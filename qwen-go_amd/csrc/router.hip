@@ -542,20 +542,25 @@ hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, 
 
 // Selection for many tokens from the matrix-core partials (bf16 router), one
 // wavefront per token.  lo_k = the k-th largest lower bound S - B among the
-// candidates of the scope; every expert whose upper bound S + B reaches it
-// (the true top k are among them: k experts have logits >= lo_k) gets its
-// reference logit computed exactly, one per lane (the sequential f32 sum of
-// model/tensors.go:77-89 on x in LDS).  They are ranked by (logit desc, index
-// asc), which is the reference's order (tensors.go:106-121 softmax, moe.go:44-57
-// selection) whenever consecutive ranks are equal or apart by more than the
-// f32 roundings of the softmax can merge (4 ulps of their distance to the max
-// plus 2^-20), the k-th is that far above every other expert's upper bound,
-// and no probability is subnormal; otherwise, or with more than 64
-// candidates, the token is queued in fbl ({count, tokens...}) for the exact
-// path (all logits, exact softmax), which select_exact_kernel runs with a row
-// per thread.
-// Weights: e_r = fl(exp(L_r - max)) as the reference rounds it, divided by
-// the f64 softmax sum of the partials, renormalised with moe.go:63's 1e-9.
+// experts of the scope; every expert of the scope whose upper bound S + B
+// reaches it (the true top k of the scope are among them) gets its reference
+// logit computed exactly, one per lane (the sequential f32 sum of
+// model/tensors.go:77-89 on x in LDS).  So does every expert, in the scope or
+// not, whose upper bound reaches the largest lower bound over all E: the
+// reference's softmax subtracts the largest of all E logits
+// (tensors.go:106-121), which can lie outside the scope (scope = k is the
+// reference's own selection, moe.go:45-53), and the roundings below are
+// sized from it.  The scope's candidates are ranked by (logit desc, index
+// asc), which is the reference's order (moe.go:44-57) whenever consecutive
+// ranks are equal or apart by more than the f32 roundings of the softmax can
+// merge (4 ulps of their distance to the max plus 2^-20), the k-th is that far
+// above every other upper bound in the scope and no probability is
+// subnormal; otherwise, or with more than 64 candidates, the token is queued
+// in fbl ({count, tokens...}) for the exact path (all logits, exact softmax),
+// which select_exact_kernel runs with a row per thread.
+// Weights: e_r = fl(exp(fl(L_r - max))) as the reference rounds it, divided by
+// the f64 softmax sum of the partials over all E, renormalised with moe.go:63's
+// 1e-9.
 template <int NJ>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) select_candidates_kernel(const float *__restrict__ x, DevMat router, int k,
                                                                int scope, const double *__restrict__ sb,
@@ -571,22 +576,25 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) se
   for (int i = lane * 4; i < H; i += 256)
     *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(x + (size_t)t * H + i);
   double S[NJ], B[NJ];
-  float key[NJ];  // lower bounds, rounded down to f32
+  float key[NJ];       // lower bounds in the scope, rounded down to f32
+  double glo = -INFINITY;  // the largest lower bound over all E
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
     const int e = lane + 64 * j;
-    const double2 v = e < E && e < scope ? reinterpret_cast<const double2 *>(sb + (size_t)t * E * 2)[e]
-                                         : make_double2(-INFINITY, 0.0);
+    const double2 v = e < E ? reinterpret_cast<const double2 *>(sb + (size_t)t * E * 2)[e]
+                            : make_double2(-INFINITY, 0.0);
     S[j] = v.x;
     B[j] = v.y;
     const double lo = S[j] - B[j];
+    if (e < E) glo = fmax(glo, lo);
     float f = (float)lo;
     if ((double)f > lo) {  // one f32 step down (f is finite here)
       const uint32_t u = __float_as_uint(f);
       f = f == 0.0f ? -0x1p-149f : __uint_as_float(f > 0.0f ? u - 1u : u + 1u);
     }
-    key[j] = f;
+    key[j] = e < scope ? f : -INFINITY;
   }
+  glo = wave_max_f64(glo);
   // lo_k: k rounds of a wavefront max over each lane's sorted keys
   float hk[NJ];
 #pragma unroll
@@ -616,21 +624,24 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) se
       hk[NJ - 1] = -INFINITY;
     }
   }
-  // candidates (upper bound >= lo_k), compacted into list
+  // candidates, compacted into list: in the scope with upper bound >= lo_k,
+  // or (any index) with upper bound >= glo, which includes the maximum's expert
   bool in[NJ];
   int n = 0;
-  double uo = -INFINITY;  // the largest upper bound among the others
+  double uo = -INFINITY;  // the largest upper bound among the scope's others
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
-    in[j] = S[j] != -INFINITY && S[j] + B[j] >= (double)lo_k;
+    const int e = lane + 64 * j;
+    const double up = S[j] + B[j];
+    in[j] = e < E && ((e < scope && up >= (double)lo_k) || up >= glo);
     const uint64_t m = __ballot(in[j]);
     const int idx = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-    if (in[j] && idx < 64) list[idx] = lane + 64 * j;
+    if (in[j] && idx < 64) list[idx] = e;
     n += __popcll(m);
-    if (!in[j] && S[j] != -INFINITY) uo = fmax(uo, S[j] + B[j]);
+    if (!in[j] && e < scope && e < E) uo = fmax(uo, up);
   }
   uo = wave_max_f64(uo);
-  bool ok = n <= 64 && n >= k;
+  bool ok = n <= 64;
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   if (ok) {
     float L = -INFINITY;
@@ -639,33 +650,37 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) se
       ce = list[lane];
       L = exact_row_logit<kBF16>(xs, H, router.w + (size_t)ce * H * 2, nullptr);
     }
-    // rank among the candidates: (logit desc, index asc)
+    // the reference's maximum over all E logits (its expert is listed)
+    const float Lmax = wave_max_f32(L);
+    // rank among the scope's candidates: (logit desc, index asc)
+    const bool ranked = lane < n && ce < scope;
     int rank = 0;
     for (int j = 0; j < n; j++) {
       const float Lj = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(L), j));
       const int ej = __builtin_amdgcn_readlane(ce, j);
-      rank += (Lj > L || (Lj == L && ej < ce)) ? 1 : 0;
+      rank += (ej < scope && (Lj > L || (Lj == L && ej < ce))) ? 1 : 0;
     }
-    if (lane < n) {
+    const int nsc = __popcll(__ballot(ranked));
+    if (ranked) {
       sorted_l[rank] = L;
       sorted_e[rank] = ce;
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    const float Lmax = sorted_l[0];
+    ok = nsc >= k;
     bool bad = false;
-    if (lane < k) {
+    if (ok && lane < k) {
       const float Lr = sorted_l[lane];
       // the next one down: the next candidate, and below the k-th the others' upper bounds
-      const double nxt = lane + 1 < n ? (double)sorted_l[lane + 1] : -INFINITY;
+      const double nxt = lane + 1 < nsc ? (double)sorted_l[lane + 1] : -INFINITY;
       const double below = lane == k - 1 ? fmax(nxt, uo) : nxt;
       const double X = (double)Lmax - fmin((double)Lr, below > -INFINITY ? below : (double)Lr);
       if (!((double)Lmax - (double)Lr < 80.0)) bad = true;
       if (below > -INFINITY && (double)Lr != below && !((double)Lr - below > f32_4ulps(X) + 0x1p-20)) bad = true;
       if (lane == k - 1 && uo > -INFINITY && !((double)Lr - uo > f32_4ulps(X) + 0x1p-20)) bad = true;
     }
-    ok = !__ballot(bad);
+    ok = ok && !__ballot(bad);
     if (ok) {
-      // softmax sum of the partials (the 1e-9 of moe.go:63 is relative to it)
+      // softmax sum of the partials over all E (the 1e-9 of moe.go:63 is relative to it)
       double z = 0.0;
 #pragma unroll
       for (int j = 0; j < NJ; j++)

@@ -18,8 +18,11 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-F32, BF16, INT8G32, INT4G32 = 0, 1, 2, 3
-FORMAT_NAMES = {F32: "f32", BF16: "bf16", INT8G32: "int8g32", INT4G32: "int4g32"}
+F32, BF16, INT8G32, INT4G32, INT8G32_F32S, INT4G32_F32S = 0, 1, 2, 3, 4, 5
+FORMAT_NAMES = {F32: "f32", BF16: "bf16", INT8G32: "int8g32", INT4G32: "int4g32",
+                INT8G32_F32S: "int8g32-f32scales", INT4G32_F32S: "int4g32-f32scales"}
+# the group-32 formats with the reference's own f32 scales (qwen-quant output)
+F32_SCALE_FORMATS = (INT8G32_F32S, INT4G32_F32S)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libqmoe.so")
@@ -72,6 +75,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_router_fallbacks": ([vp, vp], i32),
         "qmoe_router_rescues": ([vp, vp], i32),
         "qmoe_router_bounds_debug": ([vp, vp, i32, vp], i32),
+        "qmoe_debug_exchange_budget": ([vp, i64], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -86,7 +90,7 @@ def exported_symbols() -> list[str]:
             "qmoe_set_router", "qmoe_set_experts", "qmoe_set_shared", "qmoe_quantize_experts",
             "qmoe_quantize_device", "qmoe_forward", "qmoe_forward_device", "qmoe_dequant_debug",
             "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks",
-            "qmoe_router_rescues", "qmoe_router_bounds_debug"]
+            "qmoe_router_rescues", "qmoe_router_bounds_debug", "qmoe_debug_exchange_budget"]
 
 
 (STAGE_ROUTER, STAGE_SELECT, STAGE_GATE_UP, STAGE_SHARED_GATE_UP, STAGE_DOWN, STAGE_FUSED, STAGE_DISPATCH,
@@ -128,7 +132,9 @@ def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
 
 
 def weight_bytes(fmt: int, rows: int, cols: int) -> int:
-    per2 = {F32: 8, BF16: 4, INT8G32: 2, INT4G32: 1}[fmt]
+    """Device bytes of a (rows, cols) matrix in fmt (the f32-scale formats are
+    stored as their f32 dequantisation)."""
+    per2 = {F32: 8, BF16: 4, INT8G32: 2, INT4G32: 1, INT8G32_F32S: 8, INT4G32_F32S: 8}[fmt]
     b = rows * cols * per2 // 2
     if fmt in (INT8G32, INT4G32):
         b += rows * (cols // 32) * 2
@@ -248,6 +254,11 @@ class MoeLayer:
         n = ctypes.c_int64()
         self._check(self.lib.qmoe_router_rescues(self.h, ctypes.byref(n)))
         return int(n.value)
+
+    def set_exchange_budget(self, ticks: int) -> None:
+        """Wait budget of the T = 1 kernel's router exchange (100 MHz ticks;
+        negative: the default; 0: give up at once, making the call fail)."""
+        self._check(self.lib.qmoe_debug_exchange_budget(self.h, ticks))
 
     def device_bytes(self) -> int:
         return int(self.lib.qmoe_device_bytes(self.h))
@@ -373,17 +384,24 @@ class HostWeights:
 
 
 def _store(fmt: int, w: np.ndarray, n_mat: int, rows: int, cols: int, quantizer):
-    """f32 (n_mat, rows, cols) -> (stored array, fp16 scale bits or None)."""
+    """f32 (n_mat, rows, cols) -> (stored array, scales or None): fp16 scale
+    bits for INT8G32/INT4G32, the quantiser's f32 scales for the f32-scale
+    formats (quantizer(..., f32_scales=True))."""
     if fmt == F32:
         return np.ascontiguousarray(w, np.float32), None
     if fmt == BF16:
         return _to_bf16(w), None
-    return quantizer(8 if fmt == INT8G32 else 4, w, n_mat, rows, cols)
+    bits = 8 if fmt in (INT8G32, INT8G32_F32S) else 4
+    if fmt in F32_SCALE_FORMATS:
+        return quantizer(bits, w, n_mat, rows, cols, f32_scales=True)
+    return quantizer(bits, w, n_mat, rows, cols)
 
 
-def device_quantizer(bits: int, w: np.ndarray, n_mat: int, rows: int, cols: int):
+def device_quantizer(bits: int, w: np.ndarray, n_mat: int, rows: int, cols: int, f32_scales: bool = False):
     """Quantises on the device (qmoe_quantize_device); returns host codes and
     fp16 scale bits."""
+    if f32_scales:
+        raise ValueError("the device quantiser writes fp16 scales; quantise f32-scale formats on the host")
     import torch
     dw = torch.from_numpy(np.ascontiguousarray(w, np.float32).reshape(-1)).to("cuda")
     ncodes = n_mat * rows * (cols if bits == 8 else cols // 2)
@@ -427,3 +445,41 @@ def synthetic_weights(cfg: LayerConfig, seed: int, quantizer=device_quantizer,
 def synthetic_tokens(cfg: LayerConfig, T: int, seed: int) -> np.ndarray:
     rng = np.random.default_rng(seed + 7919)
     return rng.standard_normal((T, cfg.hidden), dtype=np.float32)
+
+
+def skewed_tokens(cfg, hw, T, seed, target):
+    """Prefill tokens with a skewed expert load: x_t = z_t + c u with a fixed
+    random unit direction u; c is chosen on the host (router logits in
+    float64) so that the busiest expert receives about `target` times the
+    median expert's load.  Returns (x, load stats)."""
+    rng = np.random.default_rng(seed)
+    u = rng.standard_normal(cfg.hidden)
+    u /= np.linalg.norm(u)
+    z = synthetic_tokens(cfg, T, seed)
+    if cfg.router_fmt == BF16:
+        r = bf16_bits_to_f32(hw.router).astype(np.float64)
+    else:
+        r = np.asarray(hw.router, np.float64)
+    r = r.reshape(cfg.n_experts, cfg.hidden)
+    zl, ul = z.astype(np.float64) @ r.T, r @ u
+
+    def load(c):
+        lg = zl + c * ul
+        top = np.argsort(-lg, axis=1, kind="stable")[:, :cfg.top_k]
+        return np.bincount(top.reshape(-1), minlength=cfg.n_experts)
+
+    def ratio(c):
+        n = load(c)
+        return n.max() / max(np.median(n), 1.0)
+
+    lo, hi = 0.0, 64.0
+    if ratio(lo) < target:
+        for _ in range(30):
+            mid = 0.5 * (lo + hi)
+            lo, hi = (mid, hi) if ratio(mid) < target else (lo, mid)
+    c = hi if ratio(lo) < target else lo
+    n = load(c)
+    x = (z + c * u[None, :]).astype(np.float32)
+    stats = {"c": round(float(c), 3), "max_load": int(n.max()), "median_load": float(np.median(n)),
+             "min_load": int(n.min()), "experts_used": int((n > 0).sum())}
+    return x, stats

@@ -117,6 +117,70 @@ def test_dequant_debug_bitexact(fmt):
         layer.close()
 
 
+@pytest.mark.parametrize("fmt", [qmoe.INT8G32_F32S, qmoe.INT4G32_F32S])
+def test_dequant_debug_f32_scales_bitexact(fmt):
+    """The reference's own quantised projections (qwen-quant writes F32
+    scales, cmd/qwen-quant/main.go:207-210): router and shared expert with f32
+    group scales.  Every stored matrix must equal quantLinear.dequantize with
+    the unrounded f32 scales (the oracle's dequantize), bit for bit."""
+    announce(f"dequant_debug f32 scales fmt={qmoe.FORMAT_NAMES[fmt]}")
+    cfg = qmoe.LayerConfig(256, 6, 2, 96, 64, 0, fmt, fmt, fmt, "dq-f32s")
+    hw = qmoe.synthetic_weights(cfg, 6, quantizer=oracle.host_quantizer)
+    assert hw.router_s.dtype == np.float32 and hw.sh_gate_s.dtype == np.float32
+    # the case that needs f32: scales that fp16 cannot hold exactly
+    assert np.any(oracle.f16_to_f32(oracle.f32_to_f16(hw.router_s)) != hw.router_s)
+    bits = 8 if fmt == qmoe.INT8G32_F32S else 4
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        H, I, E, Is = cfg.hidden, cfg.moe_inter, cfg.n_experts, cfg.shared_inter
+        cases = [(0, e, hw.gate_up[e], hw.gate_up_s[e], 2 * I, H) for e in (0, E - 1)]
+        cases += [(1, e, hw.down[e], hw.down_s[e], H, I) for e in (0, E - 1)]
+        cases += [(2, 0, hw.router, hw.router_s, E, H), (3, 0, hw.sh_gate, hw.sh_gate_s, Is, H),
+                  (4, 0, hw.sh_up, hw.sh_up_s, Is, H), (5, 0, hw.sh_down, hw.sh_down_s, H, Is)]
+        for which, e, w, sc, rows, cols in cases:
+            got = layer.dequant(which, e)
+            ref = oracle.dequantize(bits, w, sc, rows, cols)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (which, e)
+    finally:
+        layer.close()
+
+
+MIXED = [
+    # (router, experts, shared): the reference's quantised checkpoints keep
+    # bf16 experts and quantise the router / shared expert with f32 scales
+    (qmoe.INT8G32_F32S, qmoe.BF16, qmoe.INT4G32_F32S),
+    (qmoe.BF16, qmoe.BF16, qmoe.INT8G32_F32S),
+    (qmoe.INT4G32_F32S, qmoe.INT4G32, qmoe.INT8G32_F32S),
+    # fp16-scale shared expert in another format than the experts
+    (qmoe.BF16, qmoe.BF16, qmoe.INT8G32),
+    (qmoe.BF16, qmoe.INT4G32, qmoe.BF16),
+    (qmoe.BF16, qmoe.INT8G32, qmoe.F32),
+]
+
+
+@pytest.mark.parametrize("fmts", MIXED, ids=lambda f: "-".join(map(str, f)))
+@pytest.mark.parametrize("T", [1, 5, 100])
+def test_f32_scale_and_mixed_formats(fmts, T):
+    """Layers whose router, experts and shared expert use different formats,
+    including the f32-scale group-32 formats: decode (T = 1, 5) and the
+    batched path (T = 100), where the shared expert's GEMMs run in their own
+    format and tile size (an f32 shared expert as a bf16 copy).  ids exact,
+    weights 1e-4, output at the bar of the path."""
+    rf, ef, sf = fmts
+    cfg = qmoe.LayerConfig(256, 16, 4, 128, 128, 16, rf, ef, sf, "mixed")
+    announce(f"mixed formats {fmts} T={T}")
+    hw = qmoe.synthetic_weights(cfg, 700 + T, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, T, 700 + T)
+    if T > 32:
+        layer = qmoe.MoeLayer(cfg)
+        try:
+            assert layer.forward_path(T) == qmoe.PATH_MFMA
+        finally:
+            layer.close()
+    check_layer(cfg, hw, x)
+
+
 # --------------------------------------------------------------- layers
 
 @pytest.mark.parametrize("scope", ["k", "E"])
@@ -469,6 +533,94 @@ def test_prefill_qwen3_shape_rows_are_independent():
     assert np.all(np.isfinite(out))
 
 
+def test_prefill_qwen3_bench_input_full_size():
+    """The input that bench.py --workload prefill times: the Qwen3-30B-A3B
+    layer (bf16, seed 2026) with the router x4 and tokens skewed so that the
+    busiest expert takes about 10x the median load, T=2048, top-8 of 128.
+    Every token's ids (exact) and weights (1e-6) against the oracle's router,
+    and 64 rows strided across the whole batch against the full oracle at the
+    MFMA bar."""
+    cfg = qmoe.CONFIGS["qwen3_30b_a3b"].with_(select_scope=128)
+    announce("prefill qwen3-30b-a3b bf16 T=2048, the bench's skewed input, all ids + strided rows vs oracle")
+    hw = qmoe.synthetic_weights(cfg, 2026, quantizer=oracle.host_quantizer, router_scale=4.0)
+    x, stats = qmoe.skewed_tokens(cfg, hw, 2048, 2026 + 1000, 10.0)
+    assert stats["max_load"] >= 5 * stats["median_load"], stats
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        assert layer.forward_path(2048) == qmoe.PATH_MFMA
+        out, ids, w = layer.forward(x)
+    finally:
+        layer.close()
+    ol = oracle.OracleLayer(hw, threads=8)
+    _, rids, rw = ol.router(x)
+    assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
+    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
+    rows = np.arange(0, 2048, 32)
+    ref, _, _ = ol.forward(x[rows])
+    err = rel_err(out[rows], ref)
+    assert err <= TOL_MFMA, f"normwise relative error {err:.3e} > {TOL_MFMA}"
+    assert np.all(np.isfinite(out))
+
+
+def test_prefill_long_prompt_chunked():
+    """An 8192-token prompt at k=8: 65536 (token, rank) pairs, more than the
+    batched path's slot tables hold, so the forward runs in chunks.  Every
+    token's ids (exact) and weights (1e-6) against the oracle's router, 64
+    rows strided across all chunks against the full oracle at the MFMA bar,
+    and the rows of the last chunk equal to a separate forward of those
+    tokens bit for bit."""
+    cfg = qmoe.CONFIGS["qwen3_30b_a3b"].with_(select_scope=128)
+    announce("prefill qwen3-30b-a3b bf16 T=8192 k=8 (chunked), all ids + strided rows vs oracle")
+    hw = qmoe.synthetic_weights(cfg, 8192, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, 8192, 8192)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(x)
+        tail, tail_ids, _ = layer.forward(np.ascontiguousarray(x[8000:]))
+    finally:
+        layer.close()
+    ol = oracle.OracleLayer(hw, threads=8)
+    _, rids, rw = ol.router(x)
+    assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
+    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
+    rows = np.arange(0, 8192, 128)
+    ref, _, _ = ol.forward(x[rows])
+    assert rel_err(out[rows], ref) <= TOL_MFMA
+    assert np.array_equal(tail_ids, ids[8000:])
+    assert np.array_equal(tail.view(np.uint32), out[8000:].view(np.uint32))
+
+
+def test_batched_certified_router_reference_scope():
+    """T x E = 2^20 with the reference's own selection (scope = k = 10 of 512)
+    and a sharpened router (x4): the matrix-core router's candidates must size
+    their roundings from the maximum over all 512 logits, which lies outside
+    the scope for most tokens.  ids exact and weights within 1e-6 of the
+    oracle's router for every token; strided rows of the output at the MFMA
+    bar."""
+    cfg = qmoe.LayerConfig(2048, 512, 10, 128, 0, 10, qmoe.BF16, qmoe.BF16, qmoe.BF16, "cert-scope-k")
+    announce("batched certified router, scope=k=10 of 512, router x4, T=2048")
+    hw = qmoe.synthetic_weights(cfg, 4242, quantizer=oracle.host_quantizer, router_scale=4.0)
+    x = qmoe.synthetic_tokens(cfg, 2048, 4242)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        assert layer.forward_path(2048) == qmoe.PATH_MFMA
+        out, ids, w = layer.forward(x)
+    finally:
+        layer.close()
+    ol = oracle.OracleLayer(hw, threads=8)
+    probs, rids, rw = ol.router(x)
+    assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
+    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
+    # the case this covers: the largest probability lies outside the scope
+    assert np.mean(np.argmax(probs, axis=1) >= 10) > 0.9
+    rows = np.arange(0, 2048, 64)
+    ref, _, _ = ol.forward(x[rows])
+    assert rel_err(out[rows], ref) <= TOL_MFMA
+
+
 @pytest.mark.parametrize("key,T_small,T_full", [("qwen3_30b_a3b_int8", 64, 512), ("qwen3_next", 48, 4096)])
 def test_prefill_quantized_shapes(key, T_small, T_full):
     """Qwen3-30B-A3B int8 experts (T=512) and the Qwen3-Next int4 layer with its
@@ -542,6 +694,49 @@ def test_batched_router_candidates_ties():
     np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
     assert list(ids[0][:4]) == [5, 3, 2, 9], ids[0]
     assert fb == 0, fb
+
+
+def test_decode_exchange_timeout_fails_that_call():
+    """The T = 1 kernel's workgroups exchange router partials with a bounded
+    wait.  With the wait budget set to zero from the host, every wait gives up
+    at once (each workgroup still finishes, on exact routing): the synchronous
+    call that hit it must fail, and the handle must work again afterwards.  An
+    asynchronous call's timeout is reported by the next call, once."""
+    import torch
+    cfg = qmoe.LayerConfig(512, 16, 4, 128, 0, 16, qmoe.BF16, qmoe.BF16, qmoe.BF16, "timeout")
+    announce("decode exchange timeout forced from the host (zero wait budget)")
+    hw = qmoe.synthetic_weights(cfg, 515, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, 4, 515)
+    ref, rids, _ = oracle.OracleLayer(hw).forward(x)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, _ = layer.forward(x[0:1])
+        assert np.array_equal(ids, rids[0:1])
+        layer.set_exchange_budget(0)
+        with pytest.raises(qmoe.QmoeError) as ei:
+            layer.forward(x[1:2])
+        assert ei.value.status == 4
+        layer.set_exchange_budget(-1)
+        out, ids, _ = layer.forward(x[2:3])
+        assert np.array_equal(ids, rids[2:3])
+        assert rel_err(out, ref[2:3]) <= TOL_F32
+        # asynchronous entry
+        st = torch.cuda.current_stream().cuda_stream
+        dx = torch.from_numpy(np.ascontiguousarray(x[3:4])).cuda()
+        dout = torch.empty_like(dx)
+        layer.set_exchange_budget(0)
+        layer.forward_device(dx.data_ptr(), 1, dout.data_ptr(), None, None, st)
+        torch.cuda.synchronize()
+        layer.set_exchange_budget(-1)
+        with pytest.raises(qmoe.QmoeError) as ei:
+            layer.forward_device(dx.data_ptr(), 1, dout.data_ptr(), None, None, st)
+        assert ei.value.status == 4
+        layer.forward_device(dx.data_ptr(), 1, dout.data_ptr(), None, None, st)
+        torch.cuda.synchronize()
+        assert rel_err(dout.cpu().numpy(), ref[3:4]) <= TOL_F32
+    finally:
+        layer.close()
 
 
 # ----------------------------------------------------------- contract
