@@ -141,6 +141,19 @@ qmoe_status qmoe_forward(qmoe_layer *layer, const float *x, int32_t T, float *ou
 qmoe_status qmoe_forward_device(qmoe_layer *layer, const float *d_x, int32_t T, float *d_out,
                                 int32_t *d_ids, float *d_weights, void *stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  qmoe_forward_device for decode-sized batches, T <= 32,
+ * with no allocation of any kind: the kernels' scratch (router partials and
+ * logits, ids and weights, the exact-path queue; at most 1 MiB for E <= 1024,
+ * k <= 64) lives in a static device array that each device holds until the
+ * process ends.  Larger T returns QMOE_ERR_UNSUPPORTED.  Every call on one
+ * device shares that array, so calls that overlap on a device (different
+ * handles on streams that are not ordered) race; order them on one stream.
+ * No profiling events are recorded by this entry. */
+qmoe_status qmoe_forward_device_noalloc(qmoe_layer *layer, const float *d_x, int32_t T, float *d_out,
+                                        int32_t *d_ids, float *d_weights, void *stream);
+
 /* Exact f32 copy of a stored weight matrix, dequantised on the device as
  * quantLinear.dequantize does (model/moe.go:134-157); bf16 widened as bf16f32.
  * which: 0 expert gate_up (2I, H), 1 expert down (H, I), 2 router (E, H),

@@ -36,8 +36,9 @@ struct DevBuf {
 };
 
 // Device scratch of one forward: router logits / partials, routing, and the
-// batched path's tables and intermediate rows (the handle's workspace, grown
-// with hipMalloc).
+// batched path's tables and intermediate rows.  Either the handle's own
+// workspace (grown with hipMalloc) or the static scratch array of
+// qmoe_forward_device_noalloc.
 struct Workspace {
   float *logits = nullptr, *wts = nullptr;
   double *sb = nullptr;
@@ -81,6 +82,8 @@ struct qmoe_layer {
   Workspace w;
   float *xbuf = nullptr, *obuf = nullptr;
   bool ws_mfma = false;
+  // this device's copy of the static scratch array (qmoe_forward_device_noalloc)
+  unsigned char *scratch = nullptr;
   unsigned int *fallbacks = nullptr;  // [0] tokens routed by the exact fallback, [1] certification rescues
   // decode (T = 1): the expert kernel computes the router partials itself and
   // exchanges them between its workgroups as tagged words (2 per expert)
@@ -107,6 +110,16 @@ struct qmoe_layer {
 namespace qmoe {
 thread_local ProfEvents g_prof;
 }
+
+// Scratch of the no-allocation entry (qmoe_forward_device_noalloc):
+// decode-sized forwards (T <= 32 tokens) only -- router partials (T, E, 2)
+// f64, logits (T, E) f32, ids and weights (T, k), the exact-path queue --
+// for E <= 1024 and k <= 64.  Each device holds its own copy of the array
+// until the process ends; every call on one device shares it.  Host code
+// never uses the array's name as an address: its device address comes from
+// hipGetSymbolAddress, once per device (scratch_address).
+constexpr size_t kScratchBytes = (size_t)1 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
 
@@ -295,6 +308,41 @@ hipError_t next_event(qmoe_layer *l, hipEvent_t *ev) {
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// This device's address of the scratch array (the device must be current).
+// Looked up once per device and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_dev[kMaxDevices] = {};
+
+hipError_t scratch_address(int dev, unsigned char **out) {
+  *out = nullptr;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_dev[dev] = static_cast<unsigned char *>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return hipSuccess;
+}
+
+// The decode-path workspace of T tokens laid out in the scratch array at
+// base; *bytes receives its size.
+Workspace scratch_workspace(unsigned char *base, int T, int E, int k, size_t *bytes) {
+  size_t off = 0;
+  auto take = [&](size_t n) { size_t o = off; off += align_up(n); return base + o; };
+  Workspace w;
+  w.sb = reinterpret_cast<double *>(take((size_t)T * E * 16));
+  w.logits = reinterpret_cast<float *>(take((size_t)T * E * 4));
+  w.ids = reinterpret_cast<int32_t *>(take((size_t)T * k * 4));
+  w.wts = reinterpret_cast<float *>(take((size_t)T * k * 4));
+  w.fbl = reinterpret_cast<int *>(take((size_t)(T + 1) * 4));
+  *bytes = off;
+  return w;
+}
+
 // An exchange timeout of the decode kernel leaves the call's output
 // untrustworthy.  The synchronous entry reports it for the call that hit it;
 // an asynchronous call's timeout is reported by the next call on the handle.
@@ -398,7 +446,7 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
 }
 
 // The kernels of one forward of T tokens on stream st, with scratch from ws.
-// profile = false records no events.
+// profile = false records no events (the no-allocation entry).
 qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, int T, float *d_out, int32_t *d_ids,
                         float *d_w, hipStream_t st, bool profile = true) {
   const qmoe_desc &d = l->d;
@@ -621,8 +669,12 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
   e = hipSetDevice(d.device);
   if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
 
+  unsigned char *scr = nullptr;
+  e = scratch_address(d.device, &scr);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "hipGetSymbolAddress of the scratch array");
   qmoe_layer *l = new qmoe_layer();
   l->d = d;
+  l->scratch = scr;
   {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, d.device) == hipSuccess && prop.multiProcessorCount > 0)
@@ -853,6 +905,29 @@ qmoe_status qmoe_forward_device(qmoe_layer *l, const float *d_x, int32_t T, floa
       return s;
   }
   return QMOE_OK;
+}
+
+qmoe_status qmoe_forward_device_noalloc(qmoe_layer *l, const float *d_x, int32_t T, float *d_out, int32_t *d_ids,
+                                        float *d_weights, void *stream) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (T < 0) return fail(l, QMOE_ERR_INVALID, "T < 0");
+  if (T == 0) return QMOE_OK;
+  if (!d_x || !d_out) return fail(l, QMOE_ERR_INVALID, "null x or out pointer");
+  if (T > kMaxGemvTokens)
+    return fail(l, QMOE_ERR_UNSUPPORTED,
+                "qmoe_forward_device_noalloc takes at most " + std::to_string(kMaxGemvTokens) + " tokens (T = " +
+                    std::to_string(T) + "); use qmoe_forward_device");
+  if (!l->scratch) return fail(l, QMOE_ERR_STATE, "no scratch array address for this device");
+  size_t bytes = 0;
+  const Workspace w = scratch_workspace(l->scratch, T, l->d.n_experts, l->d.top_k, &bytes);
+  if (bytes > kScratchBytes)
+    return fail(l, QMOE_ERR_UNSUPPORTED, "qmoe_forward_device_noalloc: " + std::to_string(bytes) +
+                                             " scratch bytes needed, " + std::to_string(kScratchBytes) + " available");
+  if ((s = take_exchange_error(l, "an earlier asynchronous forward")) != QMOE_OK) return s;
+  return run_forward(l, w, d_x, T, d_out, d_ids, d_weights, (hipStream_t)stream, false);
 }
 
 qmoe_status qmoe_forward(qmoe_layer *l, const float *x, int32_t T, float *out, int32_t *ids, float *weights) {

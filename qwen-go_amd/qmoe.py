@@ -76,6 +76,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_router_rescues": ([vp, vp], i32),
         "qmoe_router_bounds_debug": ([vp, vp, i32, vp], i32),
         "qmoe_debug_exchange_budget": ([vp, i64], i32),
+        "qmoe_forward_device_noalloc": ([vp, vp, i32, vp, vp, vp, vp], i32),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -90,7 +91,8 @@ def exported_symbols() -> list[str]:
             "qmoe_set_router", "qmoe_set_experts", "qmoe_set_shared", "qmoe_quantize_experts",
             "qmoe_quantize_device", "qmoe_forward", "qmoe_forward_device", "qmoe_dequant_debug",
             "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks",
-            "qmoe_router_rescues", "qmoe_router_bounds_debug", "qmoe_debug_exchange_budget"]
+            "qmoe_router_rescues", "qmoe_router_bounds_debug", "qmoe_debug_exchange_budget",
+            "qmoe_forward_device_noalloc"]
 
 
 (STAGE_ROUTER, STAGE_SELECT, STAGE_GATE_UP, STAGE_SHARED_GATE_UP, STAGE_DOWN, STAGE_FUSED, STAGE_DISPATCH,
@@ -212,6 +214,12 @@ class MoeLayer:
     def forward_device(self, d_x: int, T: int, d_out: int, d_ids: int | None = None,
                        d_w: int | None = None, stream: int | None = None):
         self._check(self.lib.qmoe_forward_device(self.h, d_x, T, d_out, d_ids, d_w, stream))
+
+    def forward_device_noalloc(self, d_x: int, T: int, d_out: int, d_ids: int | None = None,
+                               d_w: int | None = None, stream: int | None = None):
+        """forward_device for T <= 32 with no device allocation (the kernels'
+        scratch is a static device array shared by every call on the device)."""
+        self._check(self.lib.qmoe_forward_device_noalloc(self.h, d_x, T, d_out, d_ids, d_w, stream))
 
     def dequant(self, which: int, expert: int = 0) -> np.ndarray:
         c = self.cfg
