@@ -10,6 +10,10 @@ Honest bandwidth: the layer's weights are uploaded into several distinct copies
 and the steps rotate through them, so each round of copies reads more than
 2 x 256 MB (the Infinity Cache) of weights.
 
+The default run (--workload decode) also measures the metric's other half,
+the same layer at prefill T=2048 (router x4, skewed tokens), and reports it in
+a nested "prefill" object of the same JSON line.
+
 Also reported on the same JSON line:
   roofline      the dominant kernel's algorithmic bytes per launch divided by
                 its average duration, timed with HIP events recorded on the
@@ -65,6 +69,11 @@ def parse():
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0 = auto)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill-steps", type=int, default=100,
+                    help="decode workload: steps of the prefill half of the metric (T=2048) on the same line")
+    ap.add_argument("--prefill-warmup", type=int, default=10)
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="decode workload: leave out the prefill half of the metric")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--skew", type=float, default=10.0,
                     help="prefill: target ratio of the busiest expert's load to the median load")
@@ -145,10 +154,28 @@ def stage_flops(cfg, T):
     return f
 
 
+def host_cpu():
+    """(nproc, CPU model name) of this host."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return nproc, model
+
+
 def cpu_baseline(hw, cfg, T, scope, xs, budget_s):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    threads = min(os.cpu_count() or 1, 8)
+    nproc, model = host_cpu()
+    threads = min(nproc, 8)
     ol = oracle.OracleLayer(hw, scope=scope, threads=threads)
     # per-token cost is independent of T (one forward per token, model.go:508-514):
     # a bounded slice of at most 32 tokens per call
@@ -170,6 +197,7 @@ def cpu_baseline(hw, cfg, T, scope, xs, budget_s):
                    f"(GOMAXPROCS-equivalent min(nproc,8)), expert GEMVs single-threaded; Go is not "
                    f"installed on the box"),
         "seconds": round(dt, 2),
+        "nproc": nproc, "cpu_model": model, "gomaxprocs_equivalent": threads, "expert_gemv_threads": 1,
     }
 
 
@@ -182,9 +210,20 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               f"(the MoE block is built and measured on a single MI355X)", file=sys.stderr)
         sys.exit(2)
+    result = measure(args, args.workload, args.steps, args.warmup, args.cpu_seconds)
+    if args.workload == "decode" and not args.no_prefill:
+        # the metric's other half on the same line: the same layer at T=2048
+        pre = measure(args, "prefill", args.prefill_steps, args.prefill_warmup, args.cpu_seconds / 2)
+        result["prefill"] = {k: pre[k] for k in ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config",
+                                                  "roofline", "mfma", "layer_roofline", "cpu_baseline") if k in pre}
+    print(json.dumps(result))
+
+
+def measure(args, workload, steps, warmup, cpu_seconds):
+    """One workload: warmup, `steps` timed forwards, roofline and CPU baseline."""
     import torch
 
-    key, T, scope_kind, desc = WORKLOADS[args.workload]
+    key, T, scope_kind, desc = WORKLOADS[workload]
     cfg = qmoe.CONFIGS[key]
     scope = cfg.n_experts if scope_kind == "E" else cfg.top_k
     cfg = cfg.with_(select_scope=scope)
@@ -193,7 +232,7 @@ def main():
     sptr = stream.cuda_stream
 
     t_gen = time.perf_counter()
-    hw = qmoe.synthetic_weights(cfg, args.seed, router_scale=ROUTER_SCALE.get(args.workload, 1.0))
+    hw = qmoe.synthetic_weights(cfg, args.seed, router_scale=ROUTER_SCALE.get(workload, 1.0))
     lb = qmoe.layer_bytes(cfg)
     layer_total = lb["router"] + cfg.n_experts * lb["per_expert"] + lb["shared"]
     step_bytes_est = lb["router"] + min(cfg.n_experts, T * cfg.top_k) * lb["per_expert"] + lb["shared"]
@@ -207,7 +246,7 @@ def main():
 
     n_x = max(2, min(64, (1 << 24) // (T * cfg.hidden)))
     skew = None
-    if args.workload in ROUTER_SCALE:
+    if workload in ROUTER_SCALE:
         xs_host, stats = [], []
         for i in range(n_x):
             x, st = qmoe.skewed_tokens(cfg, hw, T, args.seed + 1000 + i, args.skew)
@@ -241,7 +280,7 @@ def main():
     for L in layers:
         L.profile_enable(all_stages)
         L.profile_read(reset=True)
-    for s in range(args.warmup):
+    for s in range(warmup):
         step(s)
     torch.cuda.synchronize()
     tot_ms = np.zeros(qmoe.STAGE_COUNT)
@@ -270,7 +309,7 @@ def main():
         L.profile_read(reset=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(args.steps):
+    for s in range(steps):
         step(s)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -281,7 +320,7 @@ def main():
         dom_ms += ms[dom]
         dom_n += int(n[dom])
     dom_avg_s = dom_ms / 1e3 / max(dom_n, 1)
-    dom_bytes = float(np.mean([per_x_bytes[s % n_x][dom] for s in range(0, args.steps, copies)]))
+    dom_bytes = float(np.mean([per_x_bytes[s % n_x][dom] for s in range(0, steps, copies)]))
     achieved = dom_bytes / dom_avg_s / 1e9
     mfma_path = layers[0].forward_path(T) == qmoe.PATH_MFMA
     dom_flops = stage_flops(cfg, T).get(dom, 0) if mfma_path else 0
@@ -296,17 +335,17 @@ def main():
         if tot_n[qmoe.STAGE_FUSED]:
             return bmap[qmoe.STAGE_ROUTER] + bmap[qmoe.STAGE_FUSED]
         return sum(v for st, v in bmap.items() if st != qmoe.STAGE_FUSED and tot_n[st])
-    layer_bytes_step = float(np.mean([layer_step_bytes(per_x_bytes[s % n_x]) for s in range(args.steps)]))
-    ms_per_step = 1e3 * elapsed / args.steps
-    layer_gbs = layer_bytes_step / (elapsed / args.steps) / 1e9
+    layer_bytes_step = float(np.mean([layer_step_bytes(per_x_bytes[s % n_x]) for s in range(steps)]))
+    ms_per_step = 1e3 * elapsed / steps
+    layer_gbs = layer_bytes_step / (elapsed / steps) / 1e9
 
     result = {
         "metric": "MoE-layer tokens/s (decode T=1, prefill T=2048) + % of HBM/MFMA roofline",
-        "value": round(T * args.steps / elapsed, 2),
+        "value": round(T * steps / elapsed, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -324,13 +363,13 @@ def main():
         "roofline": ({
             "bound": "mfma", "kernel": qmoe.STAGE_NAMES[dom], "achieved": round(mfma_tflops, 1),
             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(mfma_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": measured_traffic(args.workload, qmoe.STAGE_NAMES[dom]),
+            "traffic": measured_traffic(workload, qmoe.STAGE_NAMES[dom]),
             "flops_per_launch": int(dom_flops), "bytes_per_launch": int(dom_bytes),
             "avg_launch_us": round(dom_avg_s * 1e6, 3),
         } if mfma_bound else {
             "bound": "hbm", "kernel": qmoe.STAGE_NAMES[dom], "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(args.workload, qmoe.STAGE_NAMES[dom]),
+            "traffic": measured_traffic(workload, qmoe.STAGE_NAMES[dom]),
             "bytes_per_launch": int(dom_bytes), "avg_launch_us": round(dom_avg_s * 1e6, 3),
         }),
         "mfma": ({"kernel": qmoe.STAGE_NAMES[dom], "flops_per_launch": int(dom_flops),
@@ -344,7 +383,7 @@ def main():
     fb = sum(L.router_fallbacks() for L in layers)
     rescued = sum(L.router_rescues() for L in layers)
     result["layer_roofline"]["router_fallbacks"] = {
-        "tokens": int(fb), "rescued": int(rescued), "of_tokens": int(T * (n_x + args.warmup + args.steps)),
+        "tokens": int(fb), "rescued": int(rescued), "of_tokens": int(T * (n_x + warmup + steps)),
         "note": "tokens the certified decode router could not certify: rescued = settled by exact logits of "
                 "the candidates in doubt; tokens = routed by the full exact path"}
     if skew:
@@ -354,11 +393,13 @@ def main():
                                     "experts_used": skew["per_x"][0]["experts_used"]}
     if not args.no_cpu_baseline:
         scope_for_oracle = scope
-        result["cpu_baseline"] = cpu_baseline(hw, cfg, T, scope_for_oracle, xs_host, args.cpu_seconds)
-    print(f"# setup {gen_s:.1f}s, {copies} copies x {layer_total / 1e9:.2f} GB", file=sys.stderr)
+        result["cpu_baseline"] = cpu_baseline(hw, cfg, T, scope_for_oracle, xs_host, cpu_seconds)
+    print(f"# {workload}: setup {gen_s:.1f}s, {copies} copies x {layer_total / 1e9:.2f} GB", file=sys.stderr)
     for L in layers:
         L.close()
-    print(json.dumps(result))
+    del layers, d_x, d_out, d_ids, d_w
+    torch.cuda.empty_cache()
+    return result
 
 
 if __name__ == "__main__":

@@ -60,10 +60,10 @@ __device__ __forceinline__ bool poll_zero_flags(const uint32_t *ztag, int n, uin
   }
 }
 
-// Polls the 2E tagged router words of this call until every one carries `tag`
-// (or the wait times out after `budget` ticks, or at once for a zero budget:
-// false).  Lane l receives expert l + 64 j in S[j], B[j] (S = -inf, B = 0
-// past E).
+// Polls the E tagged router words of this call (one per expert, sb_word)
+// until every one carries `tag` (or the wait times out after `budget` ticks,
+// or at once for a zero budget: false).  Lane l receives expert l + 64 j in
+// S[j], B[j] (S = -inf, B = 0 past E).
 template <int NJ>
 __device__ __forceinline__ bool poll_router_words(const uint64_t *rtag, int E, uint32_t tag, double (&S)[NJ],
                                                   double (&B)[NJ], uint64_t budget) {
@@ -78,11 +78,9 @@ __device__ __forceinline__ bool poll_router_words(const uint64_t *rtag, int E, u
       S[j] = -INFINITY;
       B[j] = 0.0;
       if (e < E) {
-        const uint64_t ws = __hip_atomic_load(rtag + 2 * e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t wb = __hip_atomic_load(rtag + 2 * e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        mine = mine && (ws & 0xffu) == tag && (wb & 0xffu) == tag;
-        S[j] = untag_word(ws);
-        B[j] = untag_word(wb);
+        const uint64_t w = __hip_atomic_load(rtag + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        mine = mine && (w & 0xffu) == tag;
+        sb_unword(w, S[j], B[j]);
       }
     }
     if (__all(mine)) return true;
@@ -166,8 +164,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
 
   // ---- router partials computed in-kernel (T = 1): waves 1..7 of the
   // workgroups take one expert each (expert e: workgroup e % G, wave
-  // 1 + e / G) and publish {S, B} as tagged words, which carry their own
-  // validity.  Wave 7 of every workgroup zeroes its slice of out and then
+  // 1 + e / G) and publish {S, B} as one tagged word (sb_word), which carries
+  // its own validity.  Wave 7 of every workgroup zeroes its slice of out and then
   // (release) tags a per-workgroup word; every workgroup waits for all of
   // those (acquire) before its atomics into out -- off the critical path,
   // since that is long after the start.
@@ -181,12 +179,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
       if (a.fused_router == 1) router_sb_wave<kBF16, 1>(a.x, H, row, nullptr, S, B);
       else if (a.fused_router == 2) router_sb_wave<kBF16, 2>(a.x, H, row, nullptr, S, B);
       else router_sb_wave<kBF16, 4>(a.x, H, row, nullptr, S, B);
-      if (lane == 0) {
-        uint64_t ws, wb;
-        tagged_sb(S, B, a.epoch, ws, wb);
-        __hip_atomic_store(a.rtag + 2 * e, ws, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.rtag + 2 * e + 1, wb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      if (lane == 0)
+        __hip_atomic_store(a.rtag + e, sb_word(S, B, a.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (wv == kFusedBlock / 64 - 1) {
       // The zeros are agent-scope stores, which write through the L2; once

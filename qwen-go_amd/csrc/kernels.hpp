@@ -103,7 +103,7 @@ struct FusedArgs {
   int burst;                          // filled by the launcher: LDS holds the burst-mode down rows
   // T = 1, bf16 router: the kernel computes the router partials itself
   // (fused_router = router chunks per lane, 1, 2 or 4; sb null), exchanges
-  // them between its workgroups through rtag (2 words per expert) tagged with
+  // them between its workgroups through rtag (one word per expert) tagged with
   // epoch (1..255, a new value every call) and zeroes out itself, each
   // workgroup a slice, announced in ztag (one word per workgroup, at most
   // kMaxExchangeBlocks).  Every wait for those words gives up after

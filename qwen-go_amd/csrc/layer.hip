@@ -86,7 +86,7 @@ struct qmoe_layer {
   unsigned char *scratch = nullptr;
   unsigned int *fallbacks = nullptr;  // [0] tokens routed by the exact fallback, [1] certification rescues
   // decode (T = 1): the expert kernel computes the router partials itself and
-  // exchanges them between its workgroups as tagged words (2 per expert)
+  // exchanges them between its workgroups as tagged words (one per expert)
   uint64_t *rtag = nullptr;
   uint32_t rtag_epoch = 0;            // tag of the last call, 1..255
   int *xchg_err_host = nullptr;       // host-visible flag: an exchange timed out
@@ -600,7 +600,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     l->rtag_epoch = l->rtag_epoch % 255 + 1;
     f.fused_router = rcpl;
     f.rtag = l->rtag;
-    f.ztag = reinterpret_cast<uint32_t *>(l->rtag + 2 * (size_t)E);
+    f.ztag = reinterpret_cast<uint32_t *>(l->rtag + (size_t)E);
     f.epoch = l->rtag_epoch;
     f.xchg_err = l->xchg_err_dev;
     f.xchg_ticks = l->xchg_ticks;
@@ -728,7 +728,7 @@ qmoe_status qmoe_create(const qmoe_desc *desc, qmoe_layer **out) {
   }
   {
     DevBuf b;
-    b.n = (size_t)E * 16 + (size_t)kMaxExchangeBlocks * 4;  // router words, then zero flags
+    b.n = (size_t)E * 8 + (size_t)kMaxExchangeBlocks * 4;  // router words (one per expert), then zero flags
     if (hipMalloc(&b.p, b.n) != hipSuccess || hipMemset(b.p, 0, b.n) != hipSuccess) {
       (void)hipGetLastError();
       free_all(l);

@@ -94,6 +94,23 @@ __device__ __forceinline__ void router_sb_wave(const float *__restrict__ xt, int
 // words from the previous call's without a separate flag.  Dropping those 8
 // bits moves S by less than 2^-43 |S|; the published bound covers that and is
 // rounded up past its own dropped bits.
+// The decode kernel's exchange packs {S, B} into one 64-bit word: S rounded
+// to f32 in the high half; in the low half an f32 upper bound of B plus that
+// rounding, whose low 8 bits carry the call's tag (setting them only raises
+// the value after the bound is first raised by 256 f32 ulps).
+__device__ __forceinline__ uint64_t sb_word(double S, double B, uint32_t tag) {
+  const float s = (float)S;
+  const double b = B + fabs(S - (double)s);
+  const float bf = (float)b;
+  uint32_t bb = __float_as_uint(bf) + ((double)bf < b ? 1u : 0u);  // b >= 0: rounded up
+  bb = ((bb + 0x100u) & ~0xffu) | (tag & 0xffu);
+  return ((uint64_t)__float_as_uint(s) << 32) | bb;
+}
+__device__ __forceinline__ void sb_unword(uint64_t w, double &S, double &B) {
+  S = (double)__uint_as_float((uint32_t)(w >> 32));
+  B = (double)__uint_as_float((uint32_t)w);
+}
+
 __device__ __forceinline__ uint64_t tag_word(double v, uint32_t tag) {
   return ((uint64_t)__double_as_longlong(v) & ~0xffull) | tag;
 }
