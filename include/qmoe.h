@@ -232,6 +232,43 @@ qmoe_status qmoe_debug_exchange_budget(qmoe_layer *layer, int64_t ticks);
 /* Bytes of device memory held by the handle (weights + workspace). */
 int64_t qmoe_device_bytes(const qmoe_layer *layer);
 
+/* ---- dense projection: linear / quantLinear on the device ----
+ * One (out_dim, in_dim) weight matrix W, y = x @ W^T for T tokens, each output
+ * the reference's sequential f32 sum fl(s + fl(x[k] * w[k])) in k order --
+ * bit for bit.  It replaces linear.matvec / mat2D / proj
+ * (model/model.go:131-205) and quantLinear.forward (model/moe.go:159-162)
+ * for the dense MLP projections (model.go:350-358) and the LM head
+ * (model.go:519-525, tied: the embedding matrix).  Formats as above; the
+ * f32-scale formats are stored as their exact f32 dequantisation.  in_dim must
+ * be a multiple of 32 (f32 and the f32-scale formats), 64 (bf16) or 256
+ * (int8, int4); other shapes return QMOE_ERR_UNSUPPORTED.  The device copy is
+ * rearranged at upload for the GEMV (64-row blocks; the same bytes plus
+ * padding to a multiple of 64 rows).  Same threading rules as qmoe_layer. */
+typedef struct qmoe_linear qmoe_linear;
+
+qmoe_status qmoe_linear_create(int32_t out_dim, int32_t in_dim, int32_t fmt, int32_t device, qmoe_linear **out);
+void qmoe_linear_destroy(qmoe_linear *lin);
+/* Message of the last failing call on lin (NULL: the last failing
+ * qmoe_linear_create on this thread).  Never NULL. */
+const char *qmoe_linear_last_error(const qmoe_linear *lin);
+/* W (out_dim, in_dim) in the handle's format from host memory (copied). */
+qmoe_status qmoe_linear_set(qmoe_linear *lin, const void *w, const void *scales);
+/* y (T, out_dim) = x (T, in_dim) @ W^T, host pointers, synchronous. */
+qmoe_status qmoe_linear_forward(qmoe_linear *lin, const float *x, int32_t T, float *y);
+/* The same on device pointers, asynchronous on stream (NULL: the default
+ * stream); no workspace. */
+qmoe_status qmoe_linear_forward_device(qmoe_linear *lin, const float *d_x, int32_t T, float *d_y, void *stream);
+/* Greedy decode's next token (model.go:519-525 then argmax model.go:652-660)
+ * for T rows: token[t] = argmax_j (x[t] @ W^T)[j], host pointers, synchronous;
+ * logits (T, out_dim) is also written when non-NULL. */
+qmoe_status qmoe_linear_greedy(qmoe_linear *lin, const float *x, int32_t T, int32_t *token, float *logits);
+/* argmax of each row of d_v (T, n), model.go:652-660: the first index of the
+ * maximum over the non-NaN entries, 0 when v[0] is NaN or there is none.
+ * Device pointers, asynchronous on stream; uses lin's workspace. */
+qmoe_status qmoe_linear_argmax_device(qmoe_linear *lin, const float *d_v, int32_t T, int32_t n, int32_t *d_token,
+                                      void *stream);
+int64_t qmoe_linear_device_bytes(const qmoe_linear *lin);
+
 #ifdef __cplusplus
 }
 #endif

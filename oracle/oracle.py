@@ -69,6 +69,9 @@ def lib() -> ctypes.CDLL:
         L.orc_sigmoid1.argtypes = [f]
         L.orc_sigmoid1.restype = f
         L.orc_select.argtypes = [vp, i, i, i, vp, vp]
+        L.orc_argmax.argtypes = [vp, i]
+        L.orc_argmax.restype = i
+        L.orc_gemma_rmsnorm.argtypes = [vp, vp, i, f]
         L.orc_moe_forward.argtypes = [ctypes.POINTER(OrcMoe), vp, i, vp, vp, vp]
         L.orc_moe_forward.restype = i
         L.orc_moe_router.argtypes = [ctypes.POINTER(OrcMoe), vp, i, vp, vp, vp]
@@ -186,6 +189,22 @@ def select(p: np.ndarray, k: int, scope: int):
     w = np.empty(k, np.float32)
     lib().orc_select(_p(p), p.size, k, scope, _p(idx), _p(w))
     return idx, w
+
+
+def argmax(v: np.ndarray) -> int:
+    """model.go:652-660 on one row."""
+    v = np.ascontiguousarray(v, np.float32)
+    return int(lib().orc_argmax(_p(v), v.size))
+
+
+def gemma_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """gemmaRMSNormApply (tensors.go:147-157) on each row of x (T, n) or (n,)."""
+    out = np.array(x, np.float32, copy=True, order="C")
+    w = np.ascontiguousarray(w, np.float32)
+    rows = out.reshape(-1, w.size)
+    for r in rows:
+        lib().orc_gemma_rmsnorm(_p(r), _p(w), w.size, eps)
+    return out
 
 
 # ------------------------------------------------------------------ layer

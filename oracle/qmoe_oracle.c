@@ -331,6 +331,29 @@ void orc_silu(float *v, int n) {
 /* sigmoid1, model/tensors.go:97. */
 float orc_sigmoid1(float x) { return 1.0f / (1.0f + (float)exp(-(double)x)); }
 
+/* argmax, model/model.go:652-660. */
+int orc_argmax(const float *v, int n) {
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return best;
+}
+
+/* gemmaRMSNormApply, model/tensors.go:147-157.  float64(v) * float64(v) is
+ * exact; the sum rounds in f64 in index order; 1 / sqrt(s/n + eps) runs in
+ * f64 (eps widened from f32) and rounds once to f32; then
+ * x = fl(fl(x * inv) * fl(1 + w)), left to right. */
+void orc_gemma_rmsnorm(float *x, const float *w, int n, float eps) {
+    double s = 0.0;
+    for (int i = 0; i < n; i++) s += (double)x[i] * (double)x[i];
+    const float inv = (float)(1.0 / sqrt(s / (double)n + (double)eps));
+    for (int i = 0; i < n; i++) {
+        const float a = x[i] * inv;
+        const float b = 1.0f + w[i];
+        x[i] = a * b;
+    }
+}
+
 /* Selection and renormalisation, model/moe.go:44-57 and :63.  The reference
  * loop runs i < topK; generalised here to i < scope, so scope == top_k is the
  * reference bit for bit and scope == n_experts is a full stable sort. */

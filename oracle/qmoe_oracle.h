@@ -112,6 +112,13 @@ float orc_sigmoid1(float x);                              /* tensors.go:97 */
 void orc_select(const float *probs, int n_experts, int top_k, int scope, int32_t *idx,
                 float *weights);
 
+/* argmax, model.go:652-660: best = 0, moved by v[i] > v[best]. */
+int orc_argmax(const float *v, int n);
+
+/* gemmaRMSNormApply, tensors.go:147-157, in place on x (n): the sum of
+ * squares in f64, inv = float32(1 / sqrt(s/n + eps)), x = x * inv * (1 + w). */
+void orc_gemma_rmsnorm(float *x, const float *w, int n, float eps);
+
 /* moeMLP.forward (moe.go:41-99) applied to each of T tokens in turn, as
  * decodeLayers does (model.go:508-514).  x (T,H), out (T,H); ids/weights
  * (T,k) in rank order, may be NULL.  Returns 0, or -1 on bad arguments. */

@@ -187,4 +187,27 @@ hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStr
 hipError_t launch_relayout_transpose(int fmt, const uint8_t *src, const uint16_t *ss, int64_t n_mat, int rows,
                                      int cols, uint8_t *dst, uint16_t *ds, hipStream_t st);
 
+// ---- dense projection and greedy token (linear.hip) ----
+// y (T, rows) = x (T, cols) @ W^T with W (rows, cols) in f32, bf16, int8 or
+// int4 group-32 (fp16 scales), each output the sequential f32 sum of
+// linear.matvec / matmulVec / quantLinear.forward (model/model.go:131-176,
+// model/tensors.go:77-89, model/moe.go:159-162).  W is held in the lane-stream
+// layout that launch_linear_relayout writes (linear_stream_bytes bytes).
+struct LinMat {
+  const uint8_t *w = nullptr;
+  int fmt = 0, rows = 0, cols = 0;
+  int n_cu = 256;  // compute units of the device (launch shape)
+};
+int linear_step(int fmt);  // cols must be a multiple of it (32 f32, 64 bf16, 256 int8/int4)
+bool linear_supported(int fmt, int cols);  // also cols <= 40960 (x of a token in LDS)
+int linear_tokens_per_pass(int T, int cols);  // a launch covers T in passes of this many tokens
+int64_t linear_stream_bytes(int fmt, int rows, int cols);
+hipError_t launch_linear_relayout(int fmt, const uint8_t *src, const uint16_t *ss, int rows, int cols, void *dst,
+                                  hipStream_t st);
+hipError_t launch_linear(const float *x, int T, const LinMat &m, float *y, hipStream_t st);
+// argmax of each row of v (T, n) with model.go:652-660's semantics; pv/pi
+// hold T * argmax_partials(n) pairs.
+int argmax_partials(int n);
+hipError_t launch_argmax(const float *v, int T, int n, float *pv, int *pi, int32_t *out, hipStream_t st);
+
 }  // namespace qmoe

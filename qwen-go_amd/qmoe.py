@@ -77,6 +77,15 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_router_bounds_debug": ([vp, vp, i32, vp], i32),
         "qmoe_debug_exchange_budget": ([vp, i64], i32),
         "qmoe_forward_device_noalloc": ([vp, vp, i32, vp, vp, vp, vp], i32),
+        "qmoe_linear_create": ([i32, i32, i32, i32, ctypes.POINTER(vp)], i32),
+        "qmoe_linear_destroy": ([vp], None),
+        "qmoe_linear_last_error": ([vp], c),
+        "qmoe_linear_set": ([vp, vp, vp], i32),
+        "qmoe_linear_forward": ([vp, vp, i32, vp], i32),
+        "qmoe_linear_forward_device": ([vp, vp, i32, vp, vp], i32),
+        "qmoe_linear_greedy": ([vp, vp, i32, vp, vp], i32),
+        "qmoe_linear_argmax_device": ([vp, vp, i32, i32, vp, vp], i32),
+        "qmoe_linear_device_bytes": ([vp], i64),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -92,7 +101,10 @@ def exported_symbols() -> list[str]:
             "qmoe_quantize_device", "qmoe_forward", "qmoe_forward_device", "qmoe_dequant_debug",
             "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks",
             "qmoe_router_rescues", "qmoe_router_bounds_debug", "qmoe_debug_exchange_budget",
-            "qmoe_forward_device_noalloc"]
+            "qmoe_forward_device_noalloc",
+            "qmoe_linear_create", "qmoe_linear_destroy", "qmoe_linear_last_error", "qmoe_linear_set",
+            "qmoe_linear_forward", "qmoe_linear_forward_device", "qmoe_linear_greedy",
+            "qmoe_linear_argmax_device", "qmoe_linear_device_bytes"]
 
 
 (STAGE_ROUTER, STAGE_SELECT, STAGE_GATE_UP, STAGE_SHARED_GATE_UP, STAGE_DOWN, STAGE_FUSED, STAGE_DISPATCH,
@@ -285,6 +297,73 @@ class MoeLayer:
             self.close()
         except Exception:
             pass
+
+
+class Linear:
+    """One dense projection resident on the device (a qmoe_linear handle):
+    qwen-go's linear / quantLinear (model/model.go:106-205, model/moe.go:124-162)
+    with outputs bit-identical to its sequential f32 sums.  Used for the dense
+    MLP projections and the LM head; `greedy` adds the argmax of
+    model/model.go:652-660 on the device."""
+
+    def __init__(self, out_dim: int, in_dim: int, fmt: int, device: int = 0):
+        self.lib = load_library()
+        self.out_dim, self.in_dim, self.fmt = out_dim, in_dim, fmt
+        h = ctypes.c_void_p()
+        st = self.lib.qmoe_linear_create(out_dim, in_dim, fmt, device, ctypes.byref(h))
+        if st != 0:
+            raise QmoeError(st, self.lib.qmoe_linear_last_error(None).decode())
+        self.h = h
+
+    def _check(self, st: int):
+        if st != 0:
+            raise QmoeError(st, self.lib.qmoe_linear_last_error(self.h).decode())
+
+    def set(self, w, scales=None):
+        self._check(self.lib.qmoe_linear_set(self.h, _ptr(w), _ptr(scales)))
+
+    def forward(self, x: np.ndarray) -> np.ndarray:
+        """x (T, in) or (in,) float32 -> y (T, out) (or (out,))."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        one = x.ndim == 1
+        x2 = x.reshape(1, -1) if one else x
+        y = np.empty((x2.shape[0], self.out_dim), np.float32)
+        self._check(self.lib.qmoe_linear_forward(self.h, _ptr(x2), x2.shape[0], _ptr(y)))
+        return y[0] if one else y
+
+    def forward_device(self, d_x: int, T: int, d_y: int, stream: int | None = None):
+        self._check(self.lib.qmoe_linear_forward_device(self.h, d_x, T, d_y, stream))
+
+    def greedy(self, x: np.ndarray, logits: bool = False):
+        """Next tokens (T,) int32 of x (T, in); with logits=True also (T, out)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.in_dim)
+        T = x.shape[0]
+        tok = np.empty(T, np.int32)
+        lg = np.empty((T, self.out_dim), np.float32) if logits else None
+        self._check(self.lib.qmoe_linear_greedy(self.h, _ptr(x), T, _ptr(tok), _ptr(lg)))
+        return (tok, lg) if logits else tok
+
+    def argmax_device(self, d_v: int, T: int, n: int, d_tok: int, stream: int | None = None):
+        self._check(self.lib.qmoe_linear_argmax_device(self.h, d_v, T, n, d_tok, stream))
+
+    def device_bytes(self) -> int:
+        return int(self.lib.qmoe_linear_device_bytes(self.h))
+
+    def close(self):
+        if getattr(self, "h", None) is not None and self.h.value:
+            self.lib.qmoe_linear_destroy(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def linear_step(fmt: int) -> int:
+    """in_dim granularity of Linear (the f32-scale formats are stored as f32)."""
+    return {F32: 32, BF16: 64, INT8G32: 256, INT4G32: 256, INT8G32_F32S: 32, INT4G32_F32S: 32}[fmt]
 
 
 def quantize_device(bits: int, d_w: int, n_mat: int, rows: int, cols: int, d_codes: int,

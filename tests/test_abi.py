@@ -115,3 +115,49 @@ def test_synthetic_weights_are_seeded():
     assert a.down.shape == (4, 64, 32) and a.gate_up_s.shape == (4, 64, 2)
     assert a.sh_gate.shape == (32, 32) and a.sh_gate.dtype == np.uint8
     assert a.router.dtype == np.uint16 and a.router.shape == (4, 64)
+
+
+@pytest.mark.parametrize("out_dim, in_dim, fmt, status", [
+    (0, 64, qmoe.BF16, 1),
+    (16, -64, qmoe.BF16, 1),
+    (16, 64, 9, 1),                      # unknown format
+    (16, 100, qmoe.BF16, 5),             # not a multiple of the 64-element bf16 step
+    (16, 48, qmoe.INT8G32, 1),           # group-32 formats need in_dim % 32 == 0
+    (16, 160, qmoe.INT4G32, 5),          # int4 and int8 super-chunks are 256 elements
+    (16, 384, qmoe.INT8G32, 5),
+    (16, 48, qmoe.INT8G32_F32S, 1),
+])
+def test_linear_create_rejects_bad_shapes(out_dim, in_dim, fmt, status):
+    lib = qmoe.load_library()
+    h = ctypes.c_void_p()
+    assert lib.qmoe_linear_create(out_dim, in_dim, fmt, 0, ctypes.byref(h)) == status
+    assert not h.value
+    assert lib.qmoe_linear_last_error(None)
+    assert lib.qmoe_linear_create(16, 64, qmoe.BF16, 0, None) == 1
+
+
+def test_linear_null_handles_are_rejected():
+    lib = qmoe.load_library()
+    assert lib.qmoe_linear_set(None, None, None) == 1
+    assert lib.qmoe_linear_forward(None, None, 1, None) == 1
+    assert lib.qmoe_linear_forward_device(None, None, 1, None, None) == 1
+    assert lib.qmoe_linear_greedy(None, None, 1, None, None) == 1
+    assert lib.qmoe_linear_argmax_device(None, None, 1, 1, None, None) == 1
+    lib.qmoe_linear_destroy(None)
+    assert lib.qmoe_linear_device_bytes(None) == 0
+
+
+def test_linear_step_matches_the_library():
+    """in_dim = one step passes the shape checks (then needs a device: status 0
+    or 1); one step plus 32 elements is refused as unsupported (5)."""
+    lib = qmoe.load_library()
+    for fmt in (qmoe.F32, qmoe.BF16, qmoe.INT8G32, qmoe.INT4G32, qmoe.INT8G32_F32S, qmoe.INT4G32_F32S):
+        step = qmoe.linear_step(fmt)
+        h = ctypes.c_void_p()
+        st = lib.qmoe_linear_create(4, step, fmt, 0, ctypes.byref(h))
+        assert st in (0, 1), (fmt, st)
+        if h.value:
+            lib.qmoe_linear_destroy(h)
+        if step > 32:
+            h = ctypes.c_void_p()
+            assert lib.qmoe_linear_create(4, step + 32, fmt, 0, ctypes.byref(h)) == 5, fmt

@@ -338,3 +338,69 @@ def test_layer_linearity_and_threads(tiny):
     assert np.max(np.abs(no_routed + no_shared - full)) < 1e-5 * np.max(np.abs(full))
     f8, _, _ = oracle.OracleLayer(_HW(cfg, **base), threads=8).forward(x)
     assert np.array_equal(bits32(f8), bits32(full))
+
+
+# ------------------------------------------------- argmax and the norm
+
+def go_argmax_brute(v):
+    """The first index of the maximum over the non-NaN entries; 0 if v[0] is
+    NaN or every entry is NaN (no comparison against a NaN best succeeds)."""
+    if np.isnan(v[0]):
+        return 0
+    ok = ~np.isnan(v)
+    m = v[ok].max()
+    return int(np.flatnonzero(ok & (v == m))[0])
+
+
+def test_argmax_known_answers_and_brute_force():
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    cases = [([1, 3, 3, 2], 1), ([nan, 5, 7], 0), ([1, nan, 2], 2), ([-0.0, 0.0], 0), ([0.0, -0.0], 0),
+             ([-inf, -inf], 0), ([nan, nan], 0), ([2, nan, nan], 0), ([-1, -inf, inf, inf], 2), ([7], 0)]
+    for v, want in cases:
+        assert oracle.argmax(np.float32(v)) == want, v
+    rng = np.random.default_rng(11)
+    for _ in range(200):
+        n = int(rng.integers(1, 300))
+        v = rng.integers(-4, 5, n).astype(np.float32)  # many ties
+        v[rng.random(n) < 0.1] = np.nan
+        assert oracle.argmax(v) == go_argmax_brute(v)
+        w = v[~np.isnan(v)]
+        if w.size and not np.isnan(v[0]):
+            assert oracle.argmax(v) == int(np.flatnonzero(~np.isnan(v))[np.argmax(w)])
+
+
+def test_gemma_rmsnorm_exact_cases():
+    # s = 16, s/n = 4, 1/sqrt(4) = 0.5: every step exact
+    w = np.float32([0.0, 1.0, -0.5, 0.25])
+    out = oracle.gemma_rmsnorm(np.float32([2, 2, 2, 2]), w, 0.0)
+    assert np.array_equal(out, np.float32([1.0, 2.0, 0.5, 1.25]))
+    # eps inside the mean: 4/4 + 3 = 4 -> inv 0.5 (eps added before the /n would give 1/sqrt(1.75))
+    out = oracle.gemma_rmsnorm(np.float32([1, 1, 1, 1]), w, 3.0)
+    assert np.array_equal(out, np.float32([0.5, 1.0, 0.25, 0.625]))
+    # the sum of squares is f64: in f32, 1 + 2^-26 rounds back to 1 every time
+    # and inv would be exactly 64; in f64 the 4095 small squares count
+    x = np.full(4096, 2.0 ** -13, np.float32)
+    x[0] = 1.0
+    out = oracle.gemma_rmsnorm(x, np.zeros(4096, np.float32), 0.0)
+    want = 64.0 / np.sqrt(1.0 + 4095 * 2.0 ** -26)
+    assert out[0] < 64.0 and abs(out[0] - want) <= 2 * np.spacing(np.float32(want))
+
+
+def test_gemma_rmsnorm_vs_float64():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(12)
+    for n, eps, scale in [(2048, 1e-6, 1.0), (2048, 1e-6, 1e-3), (1024, 1e-5, 30.0), (64, 1e-2, 0.1)]:
+        x = (rng.standard_normal((3, n)) * scale).astype(np.float32)
+        w = (rng.standard_normal(n) * 0.3).astype(np.float32)
+        got = oracle.gemma_rmsnorm(x, w, eps).astype(np.float64)
+        t = torch.from_numpy(x.astype(np.float64))
+        ref = torch.nn.functional.rms_norm(t, (n,), torch.from_numpy(1.0 + w.astype(np.float64)),
+                                           eps=float(np.float32(eps))).numpy()
+        # three f32 roundings (inv, x*inv, *(1+w)) plus the f32 rounding of 1+w
+        tol = 4 * np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+        assert np.all(np.abs(got - ref) <= tol)
+    # rows are independent
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    w = rng.standard_normal(256).astype(np.float32)
+    both = oracle.gemma_rmsnorm(x, w, 1e-6)
+    assert np.array_equal(both[1], oracle.gemma_rmsnorm(x[1], w, 1e-6))
