@@ -141,6 +141,32 @@ qmoe_status qmoe_forward(qmoe_layer *layer, const float *x, int32_t T, float *ou
 qmoe_status qmoe_forward_device(qmoe_layer *layer, const float *d_x, int32_t T, float *d_out,
                                 int32_t *d_ids, float *d_weights, void *stream);
 
+/* ---- the block with its neighbours (model/model.go:506-517) ----
+ * decodeLayers normalises a copy of each token of the residual stream with the
+ * layer's post-attention GemmaRMSNorm (gemmaRMSNormApply, model/tensors.go:
+ * 147-157), runs the MoE block on it and adds the result back:
+ *   x[t] += moeMLP.forward(gemmaRMSNorm(x[t], w, eps)).
+ * qmoe_set_post_norm uploads w (H) f32 (postAttentionLayernorm) and eps
+ * (float32(RmsNormEps)); the norm is computed bit for bit as the reference
+ * does (its f64 sum of squares certified, or redone in index order).  The
+ * residual add is folded into the block's output (out starts from x), so the
+ * normed copy and the block's own output never make a round trip. */
+qmoe_status qmoe_set_post_norm(qmoe_layer *layer, const float *w, float eps);
+/* x (T, H) f32 host pointer, updated in place; ids / weights as qmoe_forward.
+ * Synchronous. */
+qmoe_status qmoe_forward_residual(qmoe_layer *layer, float *x, int32_t T, int32_t *ids, float *weights);
+/* Device pointers, asynchronous on stream: d_out = d_x + block(norm(d_x));
+ * d_out may be d_x (in place). */
+qmoe_status qmoe_forward_residual_device(qmoe_layer *layer, const float *d_x, int32_t T, float *d_out,
+                                         int32_t *d_ids, float *d_weights, void *stream);
+/* Tokens whose norm recomputed its sum of squares in index order (the
+ * certification did not settle the f32 rounding), since create. */
+qmoe_status qmoe_norm_recomputes(qmoe_layer *layer, int64_t *count);
+/* The norm alone on host pointers, x (T, H) -> xn (T, H): for bit-exact tests. */
+qmoe_status qmoe_norm_debug(qmoe_layer *layer, const float *x, int32_t T, float *xn);
+/* on != 0: every norm takes the index-order path (tests of that path). */
+qmoe_status qmoe_debug_norm_sequential(qmoe_layer *layer, int32_t on);
+
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  qmoe_forward_device for decode-sized batches, T <= 32,

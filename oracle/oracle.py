@@ -268,6 +268,13 @@ class OracleLayer:
             raise ValueError("oracle rejected the layer description")
         return out, ids, w
 
+    def forward_residual(self, x: np.ndarray, norm_w: np.ndarray, eps: float):
+        """decodeLayers' MLP step (model/model.go:506-517): x + forward(gemmaRMSNorm(x)),
+        the add in f32."""
+        x = np.ascontiguousarray(x, np.float32)
+        out, ids, w = self.forward(gemma_rmsnorm(x, norm_w, eps))
+        return (x + out).astype(np.float32), ids, w, out
+
     def router(self, x: np.ndarray):
         x = np.ascontiguousarray(x, np.float32)
         T = x.shape[0]

@@ -165,7 +165,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   // ---- router partials computed in-kernel (T = 1): waves 1..7 of the
   // workgroups take one expert each (expert e: workgroup e % G, wave
   // 1 + e / G) and publish {S, B} as one tagged word (sb_word), which carries
-  // its own validity.  Wave 7 of every workgroup zeroes its slice of out and then
+  // its own validity.  Wave 7 of every workgroup initialises its slice of out
+  // (to the residual stream when given, else 0) and then
   // (release) tags a per-workgroup word; every workgroup waits for all of
   // those (acquire) before its atomics into out -- off the critical path,
   // since that is long after the start.
@@ -189,7 +190,7 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
       // write back the whole L2 and stall the router rows' loads).
       const int Z = (H + G - 1) / G;
       for (int j = blockIdx.x * Z + lane; j < min(H, (int)blockIdx.x * Z + Z); j += 64)
-        __hip_atomic_store(a.out + j, 0.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.out + j, a.resid ? a.resid[j] : 0.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       if (lane == 0) __hip_atomic_store(a.ztag + blockIdx.x, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

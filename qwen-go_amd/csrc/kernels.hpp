@@ -52,6 +52,7 @@ hipError_t launch_router_logits(const float *x, int T, const DevMat &router, flo
 // given, is zeroed for the fused expert kernel.
 bool router_certified_supported(const DevMat &router);
 hipError_t launch_router_sb(const float *x, int T, const DevMat &router, double *sb, float *zero_out,
+                            const float *resid,
                             hipStream_t st);
 // Certified router partials for T > 32 on the matrix cores (bf16 router, H a
 // multiple of 64, at most 8192): the same sb as launch_router_sb, from x split
@@ -97,6 +98,7 @@ struct FusedArgs {
   float *weights;                     // (T, k)
   unsigned int *fallbacks;
   float *out;                         // (T, H), accumulated
+  const float *resid;                 // (T, H) residual stream out starts from (null: 0); may be out
   int k_routed, with_shared;          // ranks of this launch
   int n_cu;                           // compute units of the device
   int nb, rb;                         // filled by the launcher: blocks per token, rows per block
@@ -130,6 +132,15 @@ int fused_exchange_blocks(const FusedArgs &a, int *resident);
 bool fused_supported(int fmt, int H, int E);  // the LDS plan fits
 hipError_t launch_zero(float *p, int64_t n, hipStream_t st);
 
+// ---- post-attention norm (norm.hip) ----
+// xn (T, n) = gemmaRMSNormApply(x, w, eps) per token (model/tensors.go:147-157),
+// bit for bit; redo (may be null) counts tokens whose certified sum of squares
+// had to be recomputed in index order (every token when force_seq).
+hipError_t launch_gemma_norm(const float *x, int T, int n, const float *w, float eps, float *xn, unsigned int *redo,
+                             bool force_seq, hipStream_t st);
+// dst (n floats) = src; nothing when they are the same.
+hipError_t launch_copy(const float *src, float *dst, int64_t n, hipStream_t st);
+
 // ---- prefill: dispatch, grouped MFMA GEMMs, combine (prefill.hip) ----
 // Slots: the T*k (token, rank) pairs grouped by expert, then the shared
 // expert's T slots (group E) in token order.
@@ -157,6 +168,7 @@ struct PrefillArgs {
   const uint16_t *sgate_s, *sup_s, *sdown_s;
   uint16_t *act;                // (slots, Imax) SwiGLU output, bf16
   uint16_t *y;                  // (slots, H) weighted expert outputs, bf16
+  const float *resid;           // (T, H) added to the combined output (null: none); may be out
 };
 bool prefill_supported(int expert_fmt, int H, int I, int Is);
 // The format the batched path keeps the shared expert in: its own when the

@@ -49,6 +49,7 @@ struct Workspace {
   float *sg = nullptr;
   uint16_t *y = nullptr;
   PrefillPlan plan{};
+  float *xn = nullptr;  // (T, H) normed x of the residual entries
 };
 
 }  // namespace
@@ -84,7 +85,13 @@ struct qmoe_layer {
   bool ws_mfma = false;
   // this device's copy of the static scratch array (qmoe_forward_device_noalloc)
   unsigned char *scratch = nullptr;
-  unsigned int *fallbacks = nullptr;  // [0] tokens routed by the exact fallback, [1] certification rescues
+  // [0] tokens routed by the exact fallback, [1] certification rescues,
+  // [2] tokens whose norm recomputed its sum of squares in index order
+  unsigned int *fallbacks = nullptr;
+  // post-attention GemmaRMSNorm of the residual entries (qmoe_set_post_norm)
+  float *norm_w = nullptr;
+  float norm_eps = 0.0f;
+  bool has_norm = false, norm_force_seq = false;
   // decode (T = 1): the expert kernel computes the router partials itself and
   // exchanges them between its workgroups as tagged words (one per expert)
   uint64_t *rtag = nullptr;
@@ -380,6 +387,7 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_o = take((size_t)nT * d.hidden * 4);
   size_t o_sb = take((size_t)nT * d.n_experts * 16);
   size_t o_fbl = take((size_t)(nT + 1) * 4);      // tokens queued for the exact routing path
+  size_t o_xn = take((size_t)nT * d.hidden * 4);  // normed x (residual entries)
   const bool want_mfma = mfma || l->ws_mfma;
   const size_t pairs = (size_t)nT * d.top_k, slots = pairs + (size_t)nT;
   const int bm = prefill_tile_slots(l->gu.fmt);
@@ -425,6 +433,7 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   l->obuf = (float *)(b + o_o);
   w.sb = (double *)(b + o_sb);
   w.fbl = (int *)(b + o_fbl);
+  w.xn = (float *)(b + o_xn);
   l->ws_mfma = want_mfma;
   if (want_mfma) {
     w.xb = (uint16_t *)(b + o_xb);
@@ -446,9 +455,11 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
 }
 
 // The kernels of one forward of T tokens on stream st, with scratch from ws.
-// profile = false records no events (the no-allocation entry).
+// profile = false records no events (the no-allocation entry).  resid: the
+// residual stream (T, H) out starts from instead of zero (may be out itself);
+// every kernel reads only d_x besides, so out may alias resid.
 qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, int T, float *d_out, int32_t *d_ids,
-                        float *d_w, hipStream_t st, bool profile = true) {
+                        float *d_w, hipStream_t st, bool profile = true, const float *resid = nullptr) {
   const qmoe_desc &d = l->d;
   if (!l->has_router || !l->has_experts || (d.shared_inter > 0 && !l->has_shared))
     return fail(l, QMOE_ERR_STATE, "weights not uploaded (router, experts and shared expert are required)");
@@ -518,6 +529,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     }
     pa.act = ws.act;
     pa.y = ws.y;
+    pa.resid = resid;
     STAGE(l, QMOE_STAGE_DISPATCH, st, launch_prefill_dispatch(pa, ids, wts, d_x, l->shared_gate, ws.sg, st),
           "dispatch launch");
     STAGE(l, QMOE_STAGE_GATE_UP, st, launch_prefill_gate_up(pa, false, st), "gate_up launch");
@@ -557,10 +569,11 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
   if (fused_router) {
     // nothing to launch before the expert kernel
   } else if (cert) {
-    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, ws.sb, d_out, st), "router launch");
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, ws.sb, d_out, resid, st), "router launch");
   } else {
     if (qmoe_status rs = route_many()) return rs;
-    HIP_TRY(l, launch_zero(d_out, (int64_t)T * H, st), "zero launch");
+    if (resid) HIP_TRY(l, launch_copy(resid, d_out, (int64_t)T * H, st), "residual copy launch");
+    else HIP_TRY(l, launch_zero(d_out, (int64_t)T * H, st), "zero launch");
   }
   FusedArgs f{};
   f.x = d_x;
@@ -606,6 +619,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     f.xchg_ticks = l->xchg_ticks;
   }
   f.out = d_out;
+  f.resid = resid;
   f.k_routed = k;
   f.with_shared = Is > 0 && l->sgate.fmt == l->gu.fmt;
   f.n_cu = l->n_cu;
@@ -907,6 +921,135 @@ qmoe_status qmoe_forward_device(qmoe_layer *l, const float *d_x, int32_t T, floa
   return QMOE_OK;
 }
 
+qmoe_status qmoe_set_post_norm(qmoe_layer *l, const float *w, float eps) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (!w) return fail(l, QMOE_ERR_INVALID, "null norm weight pointer");
+  const size_t n = (size_t)l->d.hidden * 4;
+  if (!l->norm_w) {
+    DevBuf b;
+    b.n = n;
+    if (hipMalloc(&b.p, b.n) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(l, QMOE_ERR_NOMEM, "hipMalloc of the norm weight failed");
+    }
+    l->owned.push_back(b);
+    l->weight_bytes += (int64_t)n;
+    l->norm_w = (float *)b.p;
+  }
+  HIP_TRY(l, hipMemcpy(l->norm_w, w, n, hipMemcpyHostToDevice), "norm weight upload");
+  l->norm_eps = eps;
+  l->has_norm = true;
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_forward_residual_device(qmoe_layer *l, const float *d_x, int32_t T, float *d_out, int32_t *d_ids,
+                                         float *d_weights, void *stream) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (T < 0) return fail(l, QMOE_ERR_INVALID, "T < 0");
+  if (!l->has_norm) return fail(l, QMOE_ERR_STATE, "post-attention norm not uploaded (qmoe_set_post_norm)");
+  if (T == 0) return QMOE_OK;
+  if (!d_x || !d_out) return fail(l, QMOE_ERR_INVALID, "null x or out pointer");
+  if ((s = take_exchange_error(l, "an earlier asynchronous forward")) != QMOE_OK) return s;
+  hipStream_t st = (hipStream_t)stream;
+  const int tc = chunk_tokens(l);
+  const int H = l->d.hidden, k = l->d.top_k;
+  if ((s = ensure_workspace(l, std::min(T, tc), st)) != QMOE_OK) return s;
+  for (int t0 = 0; t0 < T; t0 += tc) {
+    const int n = std::min(tc, T - t0);
+    const float *xr = d_x + (size_t)t0 * H;
+    HIP_TRY(l, launch_gemma_norm(xr, n, H, l->norm_w, l->norm_eps, l->w.xn, l->fallbacks + 2, l->norm_force_seq, st),
+            "norm launch");
+    if ((s = run_forward(l, l->w, l->w.xn, n, d_out + (size_t)t0 * H, d_ids ? d_ids + (size_t)t0 * k : nullptr,
+                         d_weights ? d_weights + (size_t)t0 * k : nullptr, st, true, xr)) != QMOE_OK)
+      return s;
+  }
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_forward_residual(qmoe_layer *l, float *x, int32_t T, int32_t *ids, float *weights) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (T < 0) return fail(l, QMOE_ERR_INVALID, "T < 0");
+  if (!l->has_norm) return fail(l, QMOE_ERR_STATE, "post-attention norm not uploaded (qmoe_set_post_norm)");
+  if (T == 0) return QMOE_OK;
+  if (!x) return fail(l, QMOE_ERR_INVALID, "null x pointer");
+  if ((s = take_exchange_error(l, "an earlier asynchronous forward")) != QMOE_OK) return s;
+  const int tc = chunk_tokens(l);
+  const int H = l->d.hidden, k = l->d.top_k;
+  if ((s = ensure_workspace(l, std::min(T, tc), nullptr)) != QMOE_OK) return s;
+  for (int t0 = 0; t0 < T; t0 += tc) {
+    const int n = std::min(tc, T - t0);
+    const size_t xb = (size_t)n * H * 4, kb = (size_t)n * k * 4;
+    HIP_TRY(l, hipMemcpyAsync(l->xbuf, x + (size_t)t0 * H, xb, hipMemcpyHostToDevice, l->stream), "x upload");
+    HIP_TRY(l, launch_gemma_norm(l->xbuf, n, H, l->norm_w, l->norm_eps, l->w.xn, l->fallbacks + 2, l->norm_force_seq,
+                                 l->stream),
+            "norm launch");
+    // x += block(norm(x)), in place in the staging buffer
+    if ((s = run_forward(l, l->w, l->w.xn, n, l->xbuf, l->w.ids, l->w.wts, l->stream, true, l->xbuf)) != QMOE_OK)
+      return s;
+    HIP_TRY(l, hipMemcpyAsync(x + (size_t)t0 * H, l->xbuf, xb, hipMemcpyDeviceToHost, l->stream), "x download");
+    if (ids)
+      HIP_TRY(l, hipMemcpyAsync(ids + (size_t)t0 * k, l->w.ids, kb, hipMemcpyDeviceToHost, l->stream), "ids download");
+    if (weights)
+      HIP_TRY(l, hipMemcpyAsync(weights + (size_t)t0 * k, l->w.wts, kb, hipMemcpyDeviceToHost, l->stream),
+              "weights download");
+    HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+  }
+  return take_exchange_error(l, "this forward");
+}
+
+qmoe_status qmoe_norm_recomputes(qmoe_layer *l, int64_t *count) {
+  if (!l || !count) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  HIP_TRY(l, hipDeviceSynchronize(), "hipDeviceSynchronize");
+  unsigned int v = 0;
+  HIP_TRY(l, hipMemcpy(&v, l->fallbacks + 2, sizeof(v), hipMemcpyDeviceToHost), "norm counter read");
+  *count = v;
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_norm_debug(qmoe_layer *l, const float *x, int32_t T, float *xn) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (!l->has_norm) return fail(l, QMOE_ERR_STATE, "post-attention norm not uploaded (qmoe_set_post_norm)");
+  if (T < 0 || (T > 0 && (!x || !xn))) return fail(l, QMOE_ERR_INVALID, "bad x, xn or T");
+  const int H = l->d.hidden;
+  for (int t0 = 0; t0 < T;) {
+    const int n = std::min(T - t0, chunk_tokens(l));
+    if ((s = ensure_workspace(l, n, nullptr)) != QMOE_OK) return s;
+    const size_t b = (size_t)n * H * 4;
+    HIP_TRY(l, hipMemcpyAsync(l->xbuf, x + (size_t)t0 * H, b, hipMemcpyHostToDevice, l->stream), "x upload");
+    HIP_TRY(l, launch_gemma_norm(l->xbuf, n, H, l->norm_w, l->norm_eps, l->w.xn, l->fallbacks + 2,
+                                 l->norm_force_seq, l->stream),
+            "norm launch");
+    HIP_TRY(l, hipMemcpyAsync(xn + (size_t)t0 * H, l->w.xn, b, hipMemcpyDeviceToHost, l->stream), "xn download");
+    HIP_TRY(l, hipStreamSynchronize(l->stream), "hipStreamSynchronize");
+    t0 += n;
+  }
+  return QMOE_OK;
+}
+
+qmoe_status qmoe_debug_norm_sequential(qmoe_layer *l, int32_t on) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  l->norm_force_seq = on != 0;
+  return QMOE_OK;
+}
+
 qmoe_status qmoe_forward_device_noalloc(qmoe_layer *l, const float *d_x, int32_t T, float *d_out, int32_t *d_ids,
                                         float *d_weights, void *stream) {
   if (!l) return QMOE_ERR_INVALID;
@@ -1004,7 +1147,7 @@ qmoe_status qmoe_router_bounds_debug(qmoe_layer *l, const float *x, int32_t T, d
   const size_t nx = (size_t)T * l->d.hidden, nsb = (size_t)T * l->d.n_experts * 2;
   hipError_t e = hipMemcpyAsync(l->xbuf, x, nx * 4, hipMemcpyHostToDevice, l->stream);
   if (e == hipSuccess)
-    e = small ? launch_router_sb(l->xbuf, T, l->router, l->w.sb, nullptr, l->stream)
+    e = small ? launch_router_sb(l->xbuf, T, l->router, l->w.sb, nullptr, nullptr, l->stream)
               : launch_router_cert_mfma(l->xbuf, T, l->router, l->w.sb, l->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(sb_out, l->w.sb, nsb * 8, hipMemcpyDeviceToHost, l->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(l->stream);

@@ -641,7 +641,7 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
 
 __global__ void __launch_bounds__(256) combine_kernel(const uint16_t *__restrict__ y, const int32_t *__restrict__ slot_of,
                                                       int T, int k, int H, int with_shared,
-                                                      float *__restrict__ out) {
+                                                      const float *resid, float *out) {
   const int t = blockIdx.x;
   auto add4 = [](float4 &acc, uint2 v) {  // four bf16 -> f32, in column order
     acc.x += bf16_to_f32(v.x & 0xffffu);
@@ -655,6 +655,10 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t *__restrict
       add4(acc, *reinterpret_cast<const uint2 *>(y + (size_t)slot_of[(size_t)t * k + r] * H + j));
     if (with_shared)  // added after the routed sum, model/moe.go:94-96
       add4(acc, *reinterpret_cast<const uint2 *>(y + ((size_t)T * k + t) * H + j));
+    if (resid) {  // the residual add around the block, x += y (model/model.go:515-517)
+      const float4 r = *reinterpret_cast<const float4 *>(resid + (size_t)t * H + j);
+      acc = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
+    }
     *reinterpret_cast<float4 *>(out + (size_t)t * H + j) = acc;
   }
 }
@@ -732,7 +736,7 @@ hipError_t launch_prefill_down(const PrefillArgs &a, bool shared, hipStream_t st
 
 hipError_t launch_prefill_combine(const PrefillArgs &a, float *out, hipStream_t st) {
   QMOE_LAUNCH(combine_kernel, dim3(a.T), dim3(256), 0, st, a.y, a.p.slot_of, a.T, a.k, a.H,
-                     (int)(a.Is > 0), out);
+                     (int)(a.Is > 0), a.resid, out);
   return hipGetLastError();
 }
 

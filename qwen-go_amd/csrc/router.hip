@@ -239,18 +239,19 @@ hipError_t launch_softmax_select(const float *logits, int T, int E, int k, int s
 // ---------------------------------------------------------------------------
 
 // One wavefront per (token, expert) writes sb[(t, e)] = {S, B}.  Block (0, t)
-// also zeroes out[t] when zero_out != nullptr (the fused expert kernel
-// accumulates into it).
+// also initialises out[t] when zero_out != nullptr (the fused expert kernel
+// accumulates into it): to resid[t], the residual stream, when given, else 0.
 template <int FMT, int CPL>
 __global__ void __launch_bounds__(256) router_sb_kernel(const float *__restrict__ x, int H,
                                                         const uint8_t *__restrict__ w,
                                                         const uint16_t *__restrict__ s, int E,
-                                                        double *__restrict__ sb, float *__restrict__ zero_out) {
+                                                        double *__restrict__ sb, float *zero_out,
+                                                        const float *resid) {
   const int t = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int e = blockIdx.x * 4 + wave;
   if (zero_out && blockIdx.x == 0)
-    for (int i = threadIdx.x; i < H; i += 256) zero_out[(size_t)t * H + i] = 0.0f;
+    for (int i = threadIdx.x; i < H; i += 256) zero_out[(size_t)t * H + i] = resid ? resid[(size_t)t * H + i] : 0.0f;
   if (e >= E) return;
   const uint8_t *row = w + (size_t)e * fmt_matrix_bytes(FMT, 1, H);
   const uint16_t *srow = fmt_quant(FMT) ? s + (size_t)e * (H / kGroup) : nullptr;
@@ -264,12 +265,14 @@ __global__ void __launch_bounds__(256) router_sb_kernel(const float *__restrict_
 }
 
 template <int FMT>
-static bool sb_fmt(const float *x, int T, const DevMat &r, double *sb, float *zero_out, hipStream_t st) {
+static bool sb_fmt(const float *x, int T, const DevMat &r, double *sb, float *zero_out, const float *resid,
+                   hipStream_t st) {
   constexpr int EPC = Chunk<FMT>::kElems;
   const int H = r.cols, E = r.rows;
   const int cpl = (H / EPC + 63) / 64;
   dim3 grid((E + 3) / 4, T);
-#define L(C) QMOE_LAUNCH((router_sb_kernel<FMT, C>), grid, dim3(256), 0, st, x, H, r.w, r.s, E, sb, zero_out)
+#define L(C) \
+  QMOE_LAUNCH((router_sb_kernel<FMT, C>), grid, dim3(256), 0, st, x, H, r.w, r.s, E, sb, zero_out, resid)
   // at most 64 products per lane (H <= 4096)
   switch (cpl) {
   case 1: L(1); return true;
@@ -289,12 +292,12 @@ bool router_certified_supported(const DevMat &router) {
 }
 
 hipError_t launch_router_sb(const float *x, int T, const DevMat &router, double *sb, float *zero_out,
-                            hipStream_t st) {
+                            const float *resid, hipStream_t st) {
   switch (router.fmt) {
-  case kF32: sb_fmt<kF32>(x, T, router, sb, zero_out, st); break;
-  case kBF16: sb_fmt<kBF16>(x, T, router, sb, zero_out, st); break;
-  case kINT8: sb_fmt<kINT8>(x, T, router, sb, zero_out, st); break;
-  default: sb_fmt<kINT4>(x, T, router, sb, zero_out, st); break;
+  case kF32: sb_fmt<kF32>(x, T, router, sb, zero_out, resid, st); break;
+  case kBF16: sb_fmt<kBF16>(x, T, router, sb, zero_out, resid, st); break;
+  case kINT8: sb_fmt<kINT8>(x, T, router, sb, zero_out, resid, st); break;
+  default: sb_fmt<kINT4>(x, T, router, sb, zero_out, resid, st); break;
   }
   return hipGetLastError();
 }

@@ -77,6 +77,12 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_router_bounds_debug": ([vp, vp, i32, vp], i32),
         "qmoe_debug_exchange_budget": ([vp, i64], i32),
         "qmoe_forward_device_noalloc": ([vp, vp, i32, vp, vp, vp, vp], i32),
+        "qmoe_set_post_norm": ([vp, vp, ctypes.c_float], i32),
+        "qmoe_forward_residual": ([vp, vp, i32, vp, vp], i32),
+        "qmoe_forward_residual_device": ([vp, vp, i32, vp, vp, vp, vp], i32),
+        "qmoe_norm_recomputes": ([vp, vp], i32),
+        "qmoe_debug_norm_sequential": ([vp, i32], i32),
+        "qmoe_norm_debug": ([vp, vp, i32, vp], i32),
         "qmoe_linear_create": ([i32, i32, i32, i32, ctypes.POINTER(vp)], i32),
         "qmoe_linear_destroy": ([vp], None),
         "qmoe_linear_last_error": ([vp], c),
@@ -101,7 +107,8 @@ def exported_symbols() -> list[str]:
             "qmoe_quantize_device", "qmoe_forward", "qmoe_forward_device", "qmoe_dequant_debug",
             "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks",
             "qmoe_router_rescues", "qmoe_router_bounds_debug", "qmoe_debug_exchange_budget",
-            "qmoe_forward_device_noalloc",
+            "qmoe_forward_device_noalloc", "qmoe_set_post_norm", "qmoe_forward_residual",
+            "qmoe_forward_residual_device", "qmoe_norm_recomputes", "qmoe_debug_norm_sequential", "qmoe_norm_debug",
             "qmoe_linear_create", "qmoe_linear_destroy", "qmoe_linear_last_error", "qmoe_linear_set",
             "qmoe_linear_forward", "qmoe_linear_forward_device", "qmoe_linear_greedy",
             "qmoe_linear_argmax_device", "qmoe_linear_device_bytes"]
@@ -232,6 +239,39 @@ class MoeLayer:
         """forward_device for T <= 32 with no device allocation (the kernels'
         scratch is a static device array shared by every call on the device)."""
         self._check(self.lib.qmoe_forward_device_noalloc(self.h, d_x, T, d_out, d_ids, d_w, stream))
+
+    def set_post_norm(self, w, eps: float):
+        """postAttentionLayernorm (H) f32 and float32(RmsNormEps)."""
+        self._check(self.lib.qmoe_set_post_norm(self.h, _ptr(np.ascontiguousarray(w, np.float32)), eps))
+
+    def forward_residual(self, x: np.ndarray):
+        """decodeLayers' MLP step (model/model.go:506-517) for T tokens:
+        returns (x + block(gemmaRMSNorm(x)), ids, weights); x is not modified."""
+        xo = np.array(x, dtype=np.float32, copy=True, order="C")
+        T = xo.shape[0]
+        ids = np.empty((T, self.cfg.top_k), np.int32)
+        w = np.empty((T, self.cfg.top_k), np.float32)
+        self._check(self.lib.qmoe_forward_residual(self.h, _ptr(xo), T, _ptr(ids), _ptr(w)))
+        return xo, ids, w
+
+    def forward_residual_device(self, d_x: int, T: int, d_out: int, d_ids: int | None = None,
+                                d_w: int | None = None, stream: int | None = None):
+        self._check(self.lib.qmoe_forward_residual_device(self.h, d_x, T, d_out, d_ids, d_w, stream))
+
+    def norm_recomputes(self) -> int:
+        c = ctypes.c_int64()
+        self._check(self.lib.qmoe_norm_recomputes(self.h, ctypes.byref(c)))
+        return c.value
+
+    def norm(self, x: np.ndarray) -> np.ndarray:
+        """The post-attention norm alone (bit-exact check)."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self._check(self.lib.qmoe_norm_debug(self.h, _ptr(x), x.shape[0], _ptr(out)))
+        return out
+
+    def set_norm_sequential(self, on: bool) -> None:
+        self._check(self.lib.qmoe_debug_norm_sequential(self.h, int(on)))
 
     def dequant(self, which: int, expert: int = 0) -> np.ndarray:
         c = self.cfg
