@@ -26,6 +26,7 @@
 // entry.  The atomics make the order of the final f32 sums run-dependent
 // (within f32 rounding of the reference's rank-ordered sum).
 #include "gemv_common.hpp"
+#include "norm_common.hpp"
 #include "router_common.hpp"
 #include "select.hpp"
 
@@ -162,6 +163,55 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   float *lt = red + 2 * H;    // exact logits (fallback)
   unsigned char *burst_lds = smem + fused_head_bytes(H, a.E);
 
+  // ---- the post-attention norm in the prologue (T = 1, a.norm_w given):
+  // every workgroup normalises x into xs itself (gemmaRMSNormApply,
+  // model/tensors.go:147-157, certified as in norm.hip), so the router
+  // partials and the rows read the normed x without a launch of its own.
+  const bool fnorm = a.norm_w != nullptr;
+  if (fnorm) {
+    __shared__ double s_part[kFusedBlock / 64];
+    __shared__ float s_inv;
+    double sq = 0.0;
+    for (int i = threadIdx.x * 4; i < H; i += kFusedBlock * 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(a.x + i);
+      *reinterpret_cast<float4 *>(xs + i) = v;
+      sq += (double)v.x * (double)v.x;
+      sq += (double)v.y * (double)v.y;
+      sq += (double)v.z * (double)v.z;
+      sq += (double)v.w * (double)v.w;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_down(sq, off, 64);
+    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double sp = 0.0;
+      for (int i = 0; i < kFusedBlock / 64; i++) sp += s_part[i];
+      float inv;
+      if (!norm_certify(sp, H, a.norm_eps, &inv) || a.norm_force_seq) {
+        double q = 0.0;
+        for (int i = 0; i < H; i++) q += (double)xs[i] * (double)xs[i];
+        inv = norm_inv(q, H, a.norm_eps);
+        if (blockIdx.x == 0 && a.norm_redo) atomicAdd(a.norm_redo, 1u);
+      }
+      s_inv = inv;
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int i = threadIdx.x * 4; i < H; i += kFusedBlock * 4) {
+#pragma clang fp contract(off)
+      float4 v = *reinterpret_cast<const float4 *>(xs + i);
+      const float4 g = *reinterpret_cast<const float4 *>(a.norm_w + i);
+      v.x = (v.x * inv) * (1.0f + g.x);
+      v.y = (v.y * inv) * (1.0f + g.y);
+      v.z = (v.z * inv) * (1.0f + g.z);
+      v.w = (v.w * inv) * (1.0f + g.w);
+      *reinterpret_cast<float4 *>(xs + i) = v;
+    }
+    __syncthreads();
+  }
+  const float *xsrc = fnorm ? xs : a.x;  // x of token 0 for the router partials
+
   // ---- router partials computed in-kernel (T = 1): waves 1..7 of the
   // workgroups take one expert each (expert e: workgroup e % G, wave
   // 1 + e / G) and publish {S, B} as one tagged word (sb_word), which carries
@@ -177,9 +227,9 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
     if (e < a.E) {
       const uint8_t *row = a.rw + (size_t)e * fmt_matrix_bytes(kBF16, 1, H);
       double S, B;
-      if (a.fused_router == 1) router_sb_wave<kBF16, 1>(a.x, H, row, nullptr, S, B);
-      else if (a.fused_router == 2) router_sb_wave<kBF16, 2>(a.x, H, row, nullptr, S, B);
-      else router_sb_wave<kBF16, 4>(a.x, H, row, nullptr, S, B);
+      if (a.fused_router == 1) router_sb_wave<kBF16, 1>(xsrc, H, row, nullptr, S, B);
+      else if (a.fused_router == 2) router_sb_wave<kBF16, 2>(xsrc, H, row, nullptr, S, B);
+      else router_sb_wave<kBF16, 4>(xsrc, H, row, nullptr, S, B);
       if (lane == 0)
         __hip_atomic_store(a.rtag + e, sb_word(S, B, a.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -232,12 +282,12 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   const bool writer = blockIdx.x % a.nb == 0 && (a.sb || a.fused_router) && a.k_routed > 0;
 
   if (threadIdx.x < 64) s_spec[threadIdx.x] = 0;
-  if (threadIdx.x == 0) s_xready = 0;
+  if (threadIdx.x == 0) s_xready = fnorm ? (kFusedBlock - kCtl) / 64 : 0;  // the prologue filled xs
   for (int j = threadIdx.x; j < 2 * H; j += kFusedBlock) red[j] = 0.0f;
   __syncthreads();
   // Waves 1..7 load x[t] into LDS and count themselves done in s_xready; the
   // control wave starts the selection at once, without x.
-  if (!ctl) {
+  if (!ctl && !fnorm) {
     for (int i = (threadIdx.x - kCtl) * 4; i < H; i += (kFusedBlock - kCtl) * 4)
       *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.x + (size_t)t * H + i);
     if ((threadIdx.x & 63) == 0)

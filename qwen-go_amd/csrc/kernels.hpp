@@ -51,8 +51,18 @@ hipError_t launch_router_logits(const float *x, int T, const DevMat &router, flo
 // bound on the reference's sequential rounding error.  zero_out (T, H), when
 // given, is zeroed for the fused expert kernel.
 bool router_certified_supported(const DevMat &router);
+// The post-attention norm folded into launch_router_sb (w null: none): x is
+// then the residual stream, the partials use its norm, and the normed tokens
+// are stored into xn (T, H) for the expert kernel.
+struct RouterNorm {
+  const float *w = nullptr;
+  float eps = 0.0f;
+  int force_seq = 0;
+  unsigned int *redo = nullptr;
+  float *xn = nullptr;
+};
 hipError_t launch_router_sb(const float *x, int T, const DevMat &router, double *sb, float *zero_out,
-                            const float *resid,
+                            const float *resid, const RouterNorm &norm,
                             hipStream_t st);
 // Certified router partials for T > 32 on the matrix cores (bf16 router, H a
 // multiple of 64, at most 8192): the same sb as launch_router_sb, from x split
@@ -118,6 +128,12 @@ struct FusedArgs {
   int *xchg_err;
   uint64_t xchg_ticks;
   int *occ_out;                       // internal: occupancy query instead of a launch
+  // T = 1 with fused_router: x is the residual stream, normalised in the
+  // kernel's prologue with norm_w (H) and norm_eps (null: x is the input)
+  const float *norm_w;
+  float norm_eps;
+  int norm_force_seq;
+  unsigned int *norm_redo;
 };
 constexpr int kMaxExchangeBlocks = 4096;
 // Default wait for the exchanged words: 2 ms.  They normally arrive within a

@@ -454,12 +454,46 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   return QMOE_OK;
 }
 
+// T = 1 with a bf16 router of at most 4 chunks per lane: the expert kernel
+// computes the router partials itself (no router launch) and initialises out.
+// Its workgroups exchange those partials, so every one of them must be
+// resident at once (checked once per handle with the occupancy calculator).
+bool fused_router_ok(qmoe_layer *l, int T) {
+  const qmoe_desc &d = l->d;
+  const int H = d.hidden, E = d.n_experts, I = d.moe_inter, Is = d.shared_inter, k = d.top_k;
+  if (use_mfma(l, T)) return false;
+  const int rcpl = (H / 8 + 63) / 64;
+  const bool fused_router = T == 1 && l->router.fmt == kBF16 && H % 8 == 0 && (rcpl == 1 || rcpl == 2 || rcpl == 4) &&
+                            E <= 7 * l->n_cu && fused_supported(l->gu.fmt, H, E);
+  if (fused_router && l->xchg_resident < 0) {
+    FusedArgs q{};
+    q.T = 1;
+    q.H = H;
+    q.E = E;
+    q.I = I;
+    q.Is = Is;
+    q.fmt = l->gu.fmt;
+    q.k_routed = k;
+    q.with_shared = Is > 0 && l->sgate.fmt == l->gu.fmt;
+    q.n_cu = l->n_cu;
+    int resident = 0;
+    const int blocks = fused_exchange_blocks(q, &resident);
+    (void)hipGetLastError();
+    l->xchg_resident = blocks <= resident && blocks <= kMaxExchangeBlocks && E <= 7 * blocks ? 1 : 0;
+  }
+  return fused_router && l->xchg_resident == 1;
+}
+
 // The kernels of one forward of T tokens on stream st, with scratch from ws.
 // profile = false records no events (the no-allocation entry).  resid: the
-// residual stream (T, H) out starts from instead of zero (may be out itself);
-// every kernel reads only d_x besides, so out may alias resid.
+// residual stream (T, H) out starts from instead of zero (may be out itself).
+// norm: d_x is that residual stream and the block's input is its post-attention
+// norm -- computed in the decode kernel's prologue on the T = 1 exchange path,
+// else by the norm kernel into ws.xn first; the kernels then read only the
+// normed x, so out may alias resid.
 qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, int T, float *d_out, int32_t *d_ids,
-                        float *d_w, hipStream_t st, bool profile = true, const float *resid = nullptr) {
+                        float *d_w, hipStream_t st, bool profile = true, const float *resid = nullptr,
+                        bool norm = false) {
   const qmoe_desc &d = l->d;
   if (!l->has_router || !l->has_experts || (d.shared_inter > 0 && !l->has_shared))
     return fail(l, QMOE_ERR_STATE, "weights not uploaded (router, experts and shared expert are required)");
@@ -473,6 +507,30 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     ~Restore() { l->prof_mask = m; }
   } restore{l, prof_mask_saved};
   const int H = d.hidden, E = d.n_experts, k = d.top_k, I = d.moe_inter, Is = d.shared_inter;
+  // Where the norm runs: in the decode kernel's prologue (T = 1 exchange
+  // path), in the certified router kernel (T <= 32; it stores the normed
+  // tokens for the expert kernel), else in a launch of its own.
+  const bool mfma = use_mfma(l, T);
+  const bool fused_router = !mfma && fused_router_ok(l, T);
+  const bool cert = !mfma && !fused_router && T <= kMaxGemvTokens && router_certified_supported(l->router);
+  RouterNorm rnorm{};
+  const float *xin = d_x;  // the expert kernels' x
+  if (norm && !fused_router) {
+    if (cert && H % 4 == 0) {
+      rnorm.w = l->norm_w;
+      rnorm.eps = l->norm_eps;
+      rnorm.force_seq = l->norm_force_seq ? 1 : 0;
+      rnorm.redo = l->fallbacks + 2;
+      rnorm.xn = ws.xn;
+      xin = ws.xn;
+    } else {
+      STAGE(l, QMOE_STAGE_ROUTER, st,
+            launch_gemma_norm(d_x, T, H, l->norm_w, l->norm_eps, ws.xn, l->fallbacks + 2, l->norm_force_seq, st),
+            "norm launch");
+      d_x = xin = ws.xn;
+    }
+    norm = false;
+  }
 
   // routing for T > 32.  Many tokens x experts with a bf16 router: bounded
   // partials on the matrix cores, then exact logits of the candidates those
@@ -493,7 +551,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     return QMOE_OK;
   };
 
-  if (use_mfma(l, T)) {
+  if (mfma) {
     // batched path: exact routing, then dispatch, grouped GEMMs, combine
     if (qmoe_status rs = route_many()) return rs;
     PrefillArgs pa{};
@@ -541,42 +599,19 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     return QMOE_OK;
   }
 
-  // T = 1 with a bf16 router of at most 4 chunks per lane: the expert kernel
-  // computes the router partials itself (no router launch) and zeroes out.
-  // Its workgroups exchange those partials, so every one of them must be
-  // resident at once (checked once per handle with the occupancy calculator).
-  const int rcpl = (H / 8 + 63) / 64;
-  bool fused_router = T == 1 && l->router.fmt == kBF16 && H % 8 == 0 && (rcpl == 1 || rcpl == 2 || rcpl == 4) &&
-                      E <= 7 * l->n_cu && fused_supported(l->gu.fmt, H, E);
-  if (fused_router && l->xchg_resident < 0) {
-    FusedArgs q{};
-    q.T = 1;
-    q.H = H;
-    q.E = E;
-    q.I = I;
-    q.Is = Is;
-    q.fmt = l->gu.fmt;
-    q.k_routed = k;
-    q.with_shared = Is > 0 && l->sgate.fmt == l->gu.fmt;
-    q.n_cu = l->n_cu;
-    int resident = 0;
-    const int blocks = fused_exchange_blocks(q, &resident);
-    (void)hipGetLastError();
-    l->xchg_resident = blocks <= resident && blocks <= kMaxExchangeBlocks && E <= 7 * blocks ? 1 : 0;
-  }
-  fused_router = fused_router && l->xchg_resident == 1;
-  const bool cert = !fused_router && T <= kMaxGemvTokens && router_certified_supported(l->router);
+  const int rcpl = (H / 8 + 63) / 64;  // router chunks per lane of the in-kernel partials
   if (fused_router) {
     // nothing to launch before the expert kernel
   } else if (cert) {
-    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, ws.sb, d_out, resid, st), "router launch");
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_sb(d_x, T, l->router, ws.sb, d_out, resid, rnorm, st),
+          "router launch");
   } else {
     if (qmoe_status rs = route_many()) return rs;
     if (resid) HIP_TRY(l, launch_copy(resid, d_out, (int64_t)T * H, st), "residual copy launch");
     else HIP_TRY(l, launch_zero(d_out, (int64_t)T * H, st), "zero launch");
   }
   FusedArgs f{};
-  f.x = d_x;
+  f.x = xin;
   f.T = T;
   f.H = H;
   f.E = E;
@@ -620,6 +655,12 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
   }
   f.out = d_out;
   f.resid = resid;
+  if (norm) {  // T = 1 on the exchange path: the prologue normalises x
+    f.norm_w = l->norm_w;
+    f.norm_eps = l->norm_eps;
+    f.norm_force_seq = l->norm_force_seq ? 1 : 0;
+    f.norm_redo = l->fallbacks + 2;
+  }
   f.k_routed = k;
   f.with_shared = Is > 0 && l->sgate.fmt == l->gu.fmt;
   f.n_cu = l->n_cu;
@@ -630,6 +671,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     f.k_routed = 0;
     f.with_shared = 1;
     f.fused_router = 0;
+    f.norm_redo = nullptr;  // counted once, by the first launch
     STAGE(l, QMOE_STAGE_FUSED, st, launch_expert_fused(f, st), "fused shared-expert launch");
   }
   return QMOE_OK;
@@ -963,10 +1005,8 @@ qmoe_status qmoe_forward_residual_device(qmoe_layer *l, const float *d_x, int32_
   for (int t0 = 0; t0 < T; t0 += tc) {
     const int n = std::min(tc, T - t0);
     const float *xr = d_x + (size_t)t0 * H;
-    HIP_TRY(l, launch_gemma_norm(xr, n, H, l->norm_w, l->norm_eps, l->w.xn, l->fallbacks + 2, l->norm_force_seq, st),
-            "norm launch");
-    if ((s = run_forward(l, l->w, l->w.xn, n, d_out + (size_t)t0 * H, d_ids ? d_ids + (size_t)t0 * k : nullptr,
-                         d_weights ? d_weights + (size_t)t0 * k : nullptr, st, true, xr)) != QMOE_OK)
+    if ((s = run_forward(l, l->w, xr, n, d_out + (size_t)t0 * H, d_ids ? d_ids + (size_t)t0 * k : nullptr,
+                         d_weights ? d_weights + (size_t)t0 * k : nullptr, st, true, xr, true)) != QMOE_OK)
       return s;
   }
   return QMOE_OK;
@@ -989,11 +1029,9 @@ qmoe_status qmoe_forward_residual(qmoe_layer *l, float *x, int32_t T, int32_t *i
     const int n = std::min(tc, T - t0);
     const size_t xb = (size_t)n * H * 4, kb = (size_t)n * k * 4;
     HIP_TRY(l, hipMemcpyAsync(l->xbuf, x + (size_t)t0 * H, xb, hipMemcpyHostToDevice, l->stream), "x upload");
-    HIP_TRY(l, launch_gemma_norm(l->xbuf, n, H, l->norm_w, l->norm_eps, l->w.xn, l->fallbacks + 2, l->norm_force_seq,
-                                 l->stream),
-            "norm launch");
     // x += block(norm(x)), in place in the staging buffer
-    if ((s = run_forward(l, l->w, l->w.xn, n, l->xbuf, l->w.ids, l->w.wts, l->stream, true, l->xbuf)) != QMOE_OK)
+    if ((s = run_forward(l, l->w, l->xbuf, n, l->xbuf, l->w.ids, l->w.wts, l->stream, true, l->xbuf, true)) !=
+        QMOE_OK)
       return s;
     HIP_TRY(l, hipMemcpyAsync(x + (size_t)t0 * H, l->xbuf, xb, hipMemcpyDeviceToHost, l->stream), "x download");
     if (ids)
@@ -1147,7 +1185,7 @@ qmoe_status qmoe_router_bounds_debug(qmoe_layer *l, const float *x, int32_t T, d
   const size_t nx = (size_t)T * l->d.hidden, nsb = (size_t)T * l->d.n_experts * 2;
   hipError_t e = hipMemcpyAsync(l->xbuf, x, nx * 4, hipMemcpyHostToDevice, l->stream);
   if (e == hipSuccess)
-    e = small ? launch_router_sb(l->xbuf, T, l->router, l->w.sb, nullptr, nullptr, l->stream)
+    e = small ? launch_router_sb(l->xbuf, T, l->router, l->w.sb, nullptr, nullptr, RouterNorm{}, l->stream)
               : launch_router_cert_mfma(l->xbuf, T, l->router, l->w.sb, l->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(sb_out, l->w.sb, nsb * 8, hipMemcpyDeviceToHost, l->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(l->stream);

@@ -15,14 +15,11 @@
 // (a test of that path).
 #include "common.hpp"
 #include "kernels.hpp"
+#include "norm_common.hpp"
 
 namespace qmoe {
 
 constexpr int kNormThreads = 256;
-
-__device__ __forceinline__ float norm_inv(double s, int n, float eps) {
-  return (float)(1.0 / __builtin_sqrt(s / (double)n + (double)eps));
-}
 
 __global__ void __launch_bounds__(kNormThreads) gemma_norm_kernel(const float *__restrict__ x,
                                                                   const float *__restrict__ w, float eps, int n,
@@ -42,10 +39,8 @@ __global__ void __launch_bounds__(kNormThreads) gemma_norm_kernel(const float *_
   if (threadIdx.x == 0) {
     double sp = 0.0;
     for (int i = 0; i < kNormThreads / 64; i++) sp += part[i];
-    // |sp - s_ref| <= 2 gamma(n-1) s: widened to 3 n u on either side
-    const double d = 3.0 * (double)n * 0x1p-53;
-    float inv = norm_inv(sp * (1.0 - d), n, eps);
-    if (force_seq || !(inv == norm_inv(sp * (1.0 + d), n, eps))) {
+    float inv;
+    if (!norm_certify(sp, n, eps, &inv) || force_seq) {
       double q = 0.0;
       for (int i = 0; i < n; i++) q += (double)xr[i] * (double)xr[i];
       inv = norm_inv(q, n, eps);

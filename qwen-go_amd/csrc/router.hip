@@ -11,6 +11,7 @@
 #include "common.hpp"
 #include "kernels.hpp"
 #include "router_common.hpp"
+#include "norm_common.hpp"
 #include "select.hpp"
 
 #include <math.h>
@@ -241,22 +242,70 @@ hipError_t launch_softmax_select(const float *logits, int T, int E, int k, int s
 // One wavefront per (token, expert) writes sb[(t, e)] = {S, B}.  Block (0, t)
 // also initialises out[t] when zero_out != nullptr (the fused expert kernel
 // accumulates into it): to resid[t], the residual stream, when given, else 0.
+// With n.w (the post-attention norm) x is the residual stream: every block
+// normalises its token into LDS first (certified as in norm.hip) and block
+// (0, t) stores the normed token into n.xn for the expert kernel.
 template <int FMT, int CPL>
 __global__ void __launch_bounds__(256) router_sb_kernel(const float *__restrict__ x, int H,
                                                         const uint8_t *__restrict__ w,
                                                         const uint16_t *__restrict__ s, int E,
                                                         double *__restrict__ sb, float *zero_out,
-                                                        const float *resid) {
+                                                        const float *resid, RouterNorm n) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) float xl[];  // (H) the normed token, when n.w
   const int t = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int e = blockIdx.x * 4 + wave;
+  const float *xt = x + (size_t)t * H;
+  if (n.w) {
+    __shared__ double s_part[4];
+    __shared__ float s_inv;
+    double sq = 0.0;
+    for (int i = threadIdx.x * 4; i < H; i += 1024) {
+      const float4 v = *reinterpret_cast<const float4 *>(xt + i);
+      *reinterpret_cast<float4 *>(xl + i) = v;
+      sq += (double)v.x * (double)v.x;
+      sq += (double)v.y * (double)v.y;
+      sq += (double)v.z * (double)v.z;
+      sq += (double)v.w * (double)v.w;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_down(sq, off, 64);
+    if (lane == 0) s_part[wave] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const double sp = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+      float inv;
+      if (!norm_certify(sp, H, n.eps, &inv) || n.force_seq) {
+        double q = 0.0;
+        for (int i = 0; i < H; i++) q += (double)xl[i] * (double)xl[i];
+        inv = norm_inv(q, H, n.eps);
+        if (blockIdx.x == 0 && n.redo) atomicAdd(n.redo, 1u);
+      }
+      s_inv = inv;
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int i = threadIdx.x * 4; i < H; i += 1024) {
+      float4 v = *reinterpret_cast<const float4 *>(xl + i);
+      const float4 g = *reinterpret_cast<const float4 *>(n.w + i);
+      v.x = (v.x * inv) * (1.0f + g.x);
+      v.y = (v.y * inv) * (1.0f + g.y);
+      v.z = (v.z * inv) * (1.0f + g.z);
+      v.w = (v.w * inv) * (1.0f + g.w);
+      *reinterpret_cast<float4 *>(xl + i) = v;
+      if (blockIdx.x == 0) *reinterpret_cast<float4 *>(n.xn + (size_t)t * H + i) = v;
+    }
+    __syncthreads();
+    xt = xl;
+  }
   if (zero_out && blockIdx.x == 0)
     for (int i = threadIdx.x; i < H; i += 256) zero_out[(size_t)t * H + i] = resid ? resid[(size_t)t * H + i] : 0.0f;
   if (e >= E) return;
   const uint8_t *row = w + (size_t)e * fmt_matrix_bytes(FMT, 1, H);
   const uint16_t *srow = fmt_quant(FMT) ? s + (size_t)e * (H / kGroup) : nullptr;
   double S, B;
-  router_sb_wave<FMT, CPL>(x + (size_t)t * H, H, row, srow, S, B);
+  router_sb_wave<FMT, CPL>(xt, H, row, srow, S, B);
   if (lane == 0) {
     double *d = sb + ((size_t)t * E + e) * 2;
     d[0] = S;
@@ -266,13 +315,14 @@ __global__ void __launch_bounds__(256) router_sb_kernel(const float *__restrict_
 
 template <int FMT>
 static bool sb_fmt(const float *x, int T, const DevMat &r, double *sb, float *zero_out, const float *resid,
-                   hipStream_t st) {
+                   const RouterNorm &n, hipStream_t st) {
   constexpr int EPC = Chunk<FMT>::kElems;
   const int H = r.cols, E = r.rows;
   const int cpl = (H / EPC + 63) / 64;
   dim3 grid((E + 3) / 4, T);
+  const size_t lds = n.w ? (size_t)H * 4 : 0;
 #define L(C) \
-  QMOE_LAUNCH((router_sb_kernel<FMT, C>), grid, dim3(256), 0, st, x, H, r.w, r.s, E, sb, zero_out, resid)
+  QMOE_LAUNCH((router_sb_kernel<FMT, C>), grid, dim3(256), lds, st, x, H, r.w, r.s, E, sb, zero_out, resid, n)
   // at most 64 products per lane (H <= 4096)
   switch (cpl) {
   case 1: L(1); return true;
@@ -292,12 +342,12 @@ bool router_certified_supported(const DevMat &router) {
 }
 
 hipError_t launch_router_sb(const float *x, int T, const DevMat &router, double *sb, float *zero_out,
-                            const float *resid, hipStream_t st) {
+                            const float *resid, const RouterNorm &n, hipStream_t st) {
   switch (router.fmt) {
-  case kF32: sb_fmt<kF32>(x, T, router, sb, zero_out, resid, st); break;
-  case kBF16: sb_fmt<kBF16>(x, T, router, sb, zero_out, resid, st); break;
-  case kINT8: sb_fmt<kINT8>(x, T, router, sb, zero_out, resid, st); break;
-  default: sb_fmt<kINT4>(x, T, router, sb, zero_out, resid, st); break;
+  case kF32: sb_fmt<kF32>(x, T, router, sb, zero_out, resid, n, st); break;
+  case kBF16: sb_fmt<kBF16>(x, T, router, sb, zero_out, resid, n, st); break;
+  case kINT8: sb_fmt<kINT8>(x, T, router, sb, zero_out, resid, n, st); break;
+  default: sb_fmt<kINT4>(x, T, router, sb, zero_out, resid, n, st); break;
   }
   return hipGetLastError();
 }

@@ -159,3 +159,33 @@ def test_residual_device_in_place(T):
     tol = TOL_MFMA if T > 32 else TOL_F32
     for got in (host, dev):
         assert residual_err(got, ref, rout) <= tol
+
+
+@pytest.mark.parametrize("T", [1, 8, 40])
+def test_residual_forced_index_order(T):
+    """The norm's index-order path in each place it runs: the decode kernel's
+    prologue (T = 1), the certified router kernel (T = 8) and the norm kernel
+    before the batched path (T = 40).  Same routing as the certified path, the
+    same bar against the oracle, and every token counted once as recomputed."""
+    cfg = qmoe.LayerConfig(2048, 64, 4, 256, 0, 64, qmoe.BF16, qmoe.BF16, qmoe.BF16, "res-seq")
+    announce(f"residual forced index-order norm T={T}")
+    hw = qmoe.synthetic_weights(cfg, 350 + T, quantizer=oracle.host_quantizer)
+    x = residual_stream(cfg, T, 350 + T)
+    w = norm_weight(cfg.hidden, 11)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        layer.set_post_norm(w, 1e-6)
+        cert, ids_c, _ = layer.forward_residual(x)
+        before = layer.norm_recomputes()
+        layer.set_norm_sequential(True)
+        seq, ids_s, _ = layer.forward_residual(x)
+        after = layer.norm_recomputes()
+        tol = TOL_MFMA if layer.forward_path(T) == qmoe.PATH_MFMA else TOL_F32
+    finally:
+        layer.close()
+    ref, rids, _, rout = oracle.OracleLayer(hw).forward_residual(x, w, 1e-6)
+    assert np.array_equal(ids_c, rids) and np.array_equal(ids_s, rids)
+    assert after - before == T
+    for got in (cert, seq):
+        assert residual_err(got, ref, rout) <= tol
