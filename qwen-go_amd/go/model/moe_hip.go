@@ -18,13 +18,20 @@ package model
 import "C"
 
 import (
+	"encoding/json"
 	"fmt"
+	"os"
+	"path/filepath"
+	"strings"
 	"unsafe"
+
+	"tinyqwengo/safetensors"
 )
 
 // qmoeDev is the device copy of one moeMLP (a qmoe_layer handle).
 type qmoeDev struct {
-	h *C.qmoe_layer
+	h    *C.qmoe_layer
+	norm bool // post-attention norm uploaded (forwardResidualT)
 }
 
 // qmoeErr formats a failed call.  The handle's message is copied into a Go
@@ -75,8 +82,19 @@ func (m *moeMLP) uploadQmoe(device int, selectScope int) (err error) {
 		moe_inter: C.int32_t(m.nMoeMlp), select_scope: C.int32_t(selectScope), device: C.int32_t(device),
 		router_fmt: rfmt, expert_fmt: C.QMOE_BF16, shared_fmt: C.QMOE_BF16,
 	}
-	var gu, dn unsafe.Pointer
+	var gu, dn, gus, dns unsafe.Pointer
 	switch {
+	case m.packed != nil:
+		p := m.packed
+		if len(p.gateUp) == 0 || len(p.gateUpScale) == 0 || len(p.down) == 0 || len(p.downScale) == 0 {
+			return fmt.Errorf("qmoe: packed experts without codes or scales")
+		}
+		gu, gus = unsafe.Pointer(&p.gateUp[0]), unsafe.Pointer(&p.gateUpScale[0])
+		dn, dns = unsafe.Pointer(&p.down[0]), unsafe.Pointer(&p.downScale[0])
+		desc.expert_fmt = C.QMOE_INT8G32
+		if p.bits == 4 {
+			desc.expert_fmt = C.QMOE_INT4G32
+		}
 	case len(m.gateUpRaw) > 0 && len(m.downRaw) > 0:
 		gu, dn = unsafe.Pointer(&m.gateUpRaw[0]), unsafe.Pointer(&m.downRaw[0])
 	case len(m.gateUpW) > 0 && len(m.downW) > 0:
@@ -118,7 +136,7 @@ func (m *moeMLP) uploadQmoe(device int, selectScope int) (err error) {
 	if st := C.qmoe_set_router(h, rw, rs); st != C.QMOE_OK {
 		return fail(st, "router")
 	}
-	if st := C.qmoe_set_experts(h, gu, nil, dn, nil); st != C.QMOE_OK {
+	if st := C.qmoe_set_experts(h, gu, gus, dn, dns); st != C.QMOE_OK {
 		return fail(st, "experts")
 	}
 	if m.shared != nil {
@@ -158,6 +176,152 @@ func (m *moeMLP) forwardT(x []float32, T int) []float32 {
 		panic(qmoeErr(m.dev.h, st, "forward"))
 	}
 	return out
+}
+
+// setPostNormQmoe uploads the block's post-attention GemmaRMSNorm weight and
+// eps (block.postAttentionLayernorm, float32(cfg.RmsNormEps)) for
+// forwardResidualT.
+func (m *moeMLP) setPostNormQmoe(w []float32, eps float32) error {
+	if m.dev == nil {
+		return fmt.Errorf("qmoe: no device copy")
+	}
+	if len(w) != m.nEmbed {
+		return fmt.Errorf("qmoe: post-attention norm has %d values, want %d", len(w), m.nEmbed)
+	}
+	if st := C.qmoe_set_post_norm(m.dev.h, (*C.float)(unsafe.Pointer(&w[0])), C.float(eps)); st != C.QMOE_OK {
+		return qmoeErr(m.dev.h, st, "post-attention norm")
+	}
+	m.dev.norm = true
+	return nil
+}
+
+// forwardResidualT is decodeLayers' whole MLP step for T tokens, in place on
+// the residual stream x (T, nEmbed): x[t] += forward(gemmaRMSNorm(x[t]))
+// (model/model.go:506-517), with the norm and the residual add on the device.
+func (m *moeMLP) forwardResidualT(x []float32, T int) {
+	if len(x) != T*m.nEmbed {
+		panic(fmt.Sprintf("qmoe residual forward: %d values for %d tokens of %d", len(x), T, m.nEmbed))
+	}
+	st := C.qmoe_forward_residual(m.dev.h, (*C.float)(unsafe.Pointer(&x[0])), C.int32_t(T), nil, nil)
+	if st != C.QMOE_OK {
+		panic(qmoeErr(m.dev.h, st, "residual forward"))
+	}
+}
+
+// packedExperts are the stacked routed experts as stored by experts_file.py:
+// <base>.qweight I8 (E, rows, K) int8 codes or (E, rows, K/2) int4 pairs, and
+// <base>.scale F16 (E, rows, K/32).  The slices alias the shard's mmap.
+type packedExperts struct {
+	bits                int
+	gateUp, gateUpScale []byte
+	down, downScale     []byte
+}
+
+// packedManifest is quant.json with the keys experts_file.py adds; the
+// reference's quantManifest ignores them.
+type packedManifest struct {
+	Bits             int      `json:"bits"`
+	Experts          []string `json:"experts"`
+	ExpertScaleDtype string   `json:"expert_scale_dtype"`
+}
+
+// loadPackedExperts attaches the packed experts of a quantised directory to
+// the model's moeMLP blocks.  Call it after FromPretrained (whose shard mmaps
+// in m.closers stay open) and before uploadQmoe; a directory without
+// "experts" in quant.json is left alone.
+func (m *model) loadPackedExperts(dir string) error {
+	raw, err := os.ReadFile(filepath.Join(dir, "quant.json"))
+	if err != nil {
+		return nil // not a quantised directory
+	}
+	var man packedManifest
+	if err := json.Unmarshal(raw, &man); err != nil {
+		return err
+	}
+	if len(man.Experts) == 0 {
+		return nil
+	}
+	if man.Bits != 8 && man.Bits != 4 {
+		return fmt.Errorf("packed experts with %d bits", man.Bits)
+	}
+	if man.ExpertScaleDtype != "" && man.ExpertScaleDtype != "F16" {
+		return fmt.Errorf("packed expert scales %q (only F16 is defined)", man.ExpertScaleDtype)
+	}
+	shards, _ := filepath.Glob(filepath.Join(dir, "*.safetensors"))
+	for _, shard := range shards {
+		f, closer, err := openShard(shard)
+		if err != nil {
+			return err
+		}
+		m.closers = append(m.closers, closer)
+		for _, key := range f.Keys() {
+			if !strings.HasSuffix(key, ".qweight") || !strings.Contains(key, ".mlp.experts.") {
+				continue
+			}
+			base := strings.TrimSuffix(key, ".qweight")
+			qw, qshape, qdt, err := f.Raw(key)
+			if err != nil {
+				return err
+			}
+			sc, sshape, sdt, err := f.Raw(base + ".scale")
+			if err != nil {
+				return err
+			}
+			if qdt != safetensors.I8 || sdt != safetensors.F16 || len(qshape) != 3 || len(sshape) != 3 {
+				return fmt.Errorf("%s: packed experts must be I8 (E, rows, K) + F16 scales", base)
+			}
+			flat := renameKey(base)
+			layer, which, err := packedTarget(flat)
+			if err != nil {
+				return err
+			}
+			if layer < 0 || layer >= len(m.layers) {
+				return fmt.Errorf("%s: layer %d out of range", base, layer)
+			}
+			moe, ok := m.layers[layer].mlp.(*moeMLP)
+			if !ok {
+				return fmt.Errorf("%s: layer %d has no MoE block", base, layer)
+			}
+			if moe.packed == nil {
+				moe.packed = &packedExperts{bits: man.Bits}
+			}
+			k := qshape[2]
+			if man.Bits == 4 {
+				k *= 2
+			}
+			if sshape[0] != qshape[0] || sshape[1] != qshape[1] || sshape[2]*32 != k {
+				return fmt.Errorf("%s: scale shape %v does not match codes %v", base, sshape, qshape)
+			}
+			if which == "gate_up_proj" {
+				moe.packed.gateUp, moe.packed.gateUpScale = qw, sc
+			} else {
+				moe.packed.down, moe.packed.downScale = qw, sc
+			}
+		}
+	}
+	return nil
+}
+
+// packedTarget splits "layers.N.mlp.experts.<which>" into N and which.
+func packedTarget(flat string) (int, string, error) {
+	var layer int
+	var which string
+	rest := strings.TrimPrefix(flat, "layers.")
+	dot := strings.Index(rest, ".")
+	if dot <= 0 || !strings.HasPrefix(flat, "layers.") {
+		return 0, "", fmt.Errorf("unsupported packed target %q", flat)
+	}
+	for _, c := range rest[:dot] {
+		if c < '0' || c > '9' {
+			return 0, "", fmt.Errorf("bad layer index in %q", flat)
+		}
+		layer = layer*10 + int(c-'0')
+	}
+	which = strings.TrimPrefix(rest[dot:], ".mlp.experts.")
+	if which != "gate_up_proj" && which != "down_proj" {
+		return 0, "", fmt.Errorf("unsupported packed target %q", flat)
+	}
+	return layer, which, nil
 }
 
 // closeQmoe releases the device copy.
