@@ -12,7 +12,10 @@ and the steps rotate through them, so each round of copies reads more than
 
 The default run (--workload decode) also measures the metric's other half,
 the same layer at prefill T=2048 (router x4, skewed tokens), and reports it in
-a nested "prefill" object of the same JSON line.
+a nested "prefill" object of the same JSON line, and the block's neighbours in
+a "neighbours" object: the LM head GEMV (151936 x 2048 bf16, T = 1, bit-exact
+sequential sums) with its CPU baseline, and the decode step with the
+post-attention norm and the residual add folded in against the block alone.
 
 Also reported on the same JSON line:
   roofline      the dominant kernel's algorithmic bytes per launch divided by
@@ -65,7 +68,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="decode", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="decode", choices=sorted(WORKLOADS) + ["lm_head"],
+                    help="lm_head: the LM head GEMV alone (its own JSON line)")
     ap.add_argument("--copies", type=int, default=0, help="weight copies to rotate (0 = auto)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -74,6 +78,8 @@ def parse():
     ap.add_argument("--prefill-warmup", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true",
                     help="decode workload: leave out the prefill half of the metric")
+    ap.add_argument("--no-neighbours", action="store_true",
+                    help="decode workload: leave out the LM head and norm+residual measurements")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--skew", type=float, default=10.0,
                     help="prefill: target ratio of the busiest expert's load to the median load")
@@ -210,13 +216,103 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               f"(the MoE block is built and measured on a single MI355X)", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "lm_head":
+        print(json.dumps(measure_lm_head(args, steps=args.steps)))
+        return
     result = measure(args, args.workload, args.steps, args.warmup, args.cpu_seconds)
     if args.workload == "decode" and not args.no_prefill:
         # the metric's other half on the same line: the same layer at T=2048
         pre = measure(args, "prefill", args.prefill_steps, args.prefill_warmup, args.cpu_seconds / 2)
         result["prefill"] = {k: pre[k] for k in ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config",
                                                   "roofline", "mfma", "layer_roofline", "cpu_baseline") if k in pre}
+    if args.workload == "decode" and not args.no_neighbours:
+        result["neighbours"] = {"lm_head": measure_lm_head(args), "norm_residual": measure_norm_residual(args)}
     print(json.dumps(result))
+
+
+def _time_us(fn, steps, warmup):
+    """Average µs of fn() over steps calls, HIP events on torch's current
+    stream (every call here launches on that stream)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / steps
+
+
+def measure_lm_head(args, rows=151936, cols=2048, steps=200):
+    """The LM head (model/model.go:519-525): y = x @ W^T, W (151936, 2048) bf16,
+    T = 1, through qmoe_linear_forward_device; bytes = W + x + y (622 MB, more
+    than the Infinity Cache holds).  CPU baseline: the oracle's matvec, bf16
+    rows fanned out on min(nproc, 8) threads as linear.matvec does."""
+    import torch
+    rng = np.random.default_rng(args.seed + 7)
+    w = qmoe.f32_to_bf16_bits(rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
+    lin = qmoe.Linear(rows, cols, qmoe.BF16)
+    try:
+        lin.set(w)
+        x = torch.from_numpy(rng.standard_normal((1, cols), dtype=np.float32)).cuda()
+        y = torch.empty((1, rows), dtype=torch.float32, device="cuda")
+        sptr = torch.cuda.current_stream().cuda_stream
+        us = _time_us(lambda: lin.forward_device(x.data_ptr(), 1, y.data_ptr(), sptr), steps, 20)
+        tok = torch.empty(1, dtype=torch.int32, device="cuda")
+        us_argmax = _time_us(lambda: lin.argmax_device(y.data_ptr(), 1, rows, tok.data_ptr(), sptr), steps, 20)
+    finally:
+        lin.close()
+    nbytes = qmoe.weight_bytes(qmoe.BF16, rows, cols) + 4 * (rows + cols)
+    gbs = nbytes / us / 1e3
+    out = {"value": round(1e6 / us, 1), "unit": "calls/s", "us_per_call": round(us, 2),
+           "argmax_us": round(us_argmax, 2), "dtype": "f32 (bf16 weights)",
+           "config": {"workload": f"lm head GEMV ({rows}, {cols}) bf16, T=1, outputs bit-exact"},
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 3), "algorithmic_bytes": nbytes}}
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        nproc, model = host_cpu()
+        threads = min(nproc, 8)
+        xh = x.cpu().numpy()[0]
+        reps, t0 = 0, time.perf_counter()
+        while reps < 3 or (time.perf_counter() - t0 < 4.0 and reps < 50):
+            oracle.matvec(oracle.BF16, w, None, xh, rows, cols, threads=threads)
+            reps += 1
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(reps / dt, 2), "unit": "calls/s", "cores": threads, "kind": "port",
+                               "sample": f"{reps} full LM-head matvecs, C restatement of linear.matvec "
+                                         f"(model/model.go:131-176), bf16 rows on {threads} threads",
+                               "nproc": nproc, "cpu_model": model}
+    return out
+
+
+def measure_norm_residual(args, steps=400):
+    """decodeLayers' MLP step with the post-attention norm and the residual
+    add on the device (qmoe_forward_residual_device) against the block alone
+    (qmoe_forward_device), Qwen3-30B-A3B bf16 layer, T = 1, one weight copy
+    for both (the difference is what the folding costs)."""
+    import torch
+    cfg = qmoe.CONFIGS["qwen3_30b_a3b"].with_(select_scope=128)
+    hw = qmoe.synthetic_weights(cfg, args.seed)
+    L = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(L)
+        L.set_post_norm(np.random.default_rng(args.seed).standard_normal(cfg.hidden).astype(np.float32) * 0.2, 1e-6)
+        x = torch.from_numpy(qmoe.synthetic_tokens(cfg, 1, args.seed + 3) * np.float32(8.0)).cuda()
+        out = torch.empty_like(x)
+        sptr = torch.cuda.current_stream().cuda_stream
+        plain = _time_us(lambda: L.forward_device(x.data_ptr(), 1, out.data_ptr(), None, None, sptr), steps, 40)
+        res = _time_us(lambda: L.forward_residual_device(x.data_ptr(), 1, out.data_ptr(), None, None, sptr),
+                       steps, 40)
+    finally:
+        L.close()
+    return {"block_us": round(plain, 2), "norm_block_residual_us": round(res, 2),
+            "overhead_us": round(res - plain, 2),
+            "config": {"workload": "qwen3-30b-a3b moe layer decode T=1 bf16, top-8 of 128, one weight copy"}}
 
 
 def measure(args, workload, steps, warmup, cpu_seconds):

@@ -145,6 +145,29 @@ constexpr bool accumulate_in_registers() {
   return ITER > 0 && ITER * Chunk<FMT>::kElems <= 32;
 }
 
+// Phase timeline of the decode kernel, built only into the instrumented
+// library (make libqmoe_timeline.so, -DQMOE_TIMELINE): one s_memrealtime
+// stamp (100 MHz) per (workgroup, point) from the first lane of the named
+// wave, read back with qmoe_timeline_read.  The product library compiles the
+// stamps away.
+#ifdef QMOE_TIMELINE
+constexpr int kStampsPerBlock = 16;
+__device__ uint64_t g_timeline[kMaxExchangeBlocks * kStampsPerBlock];
+#define QMOE_STAMP(i, wave)                                                                \
+  do {                                                                                     \
+    if (threadIdx.x == (wave) * 64)                                                        \
+      g_timeline[blockIdx.x * kStampsPerBlock + (i)] = __builtin_amdgcn_s_memrealtime();  \
+  } while (0)
+#define QMOE_STAMP_DRAINED(i, wave)                                                        \
+  do {                                                                                     \
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                     \
+    QMOE_STAMP(i, wave);                                                                   \
+  } while (0)
+#else
+#define QMOE_STAMP(i, wave) do { } while (0)
+#define QMOE_STAMP_DRAINED(i, wave) do { } while (0)
+#endif
+
 template <int FMT, int ITER, int NJ>
 __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) {
   constexpr int EPC = Chunk<FMT>::kElems;
@@ -162,6 +185,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   float *red = xs + H;        // (2, H): the block's two runs
   float *lt = red + 2 * H;    // exact logits (fallback)
   unsigned char *burst_lds = smem + fused_head_bytes(H, a.E);
+  QMOE_STAMP(0, 0);
+  QMOE_STAMP(1, 1);
 
   // ---- the post-attention norm in the prologue (T = 1, a.norm_w given):
   // every workgroup normalises x into xs itself (gemmaRMSNormApply,
@@ -232,6 +257,7 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
       else router_sb_wave<kBF16, 4>(xsrc, H, row, nullptr, S, B);
       if (lane == 0)
         __hip_atomic_store(a.rtag + e, sb_word(S, B, a.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (wv == 1) QMOE_STAMP_DRAINED(2, 1);
     }
     if (wv == kFusedBlock / 64 - 1) {
       // The zeros are agent-scope stores, which write through the L2; once
@@ -494,6 +520,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
           }
         }
         __builtin_amdgcn_s_waitcnt(0);  // the down rows have landed in LDS
+        QMOE_STAMP(6, 1);
+        QMOE_STAMP(13, 7);
         float acc0[IT][EPC], acc1[IT][EPC];
 #pragma unroll
         for (int c = 0; c < IT; c++)
@@ -705,7 +733,9 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
         gi = writer ? a.ids : nullptr;
         gw = writer ? a.weights : nullptr;
         if (poll_router_words<NJ>(a.rtag, a.E, a.epoch, S, B, a.xchg_ticks)) {
+          QMOE_STAMP(3, 0);
           rescue = !certified_select_regs<NJ>(S, B, a.E, a.k, a.scope, gi, gw, s_ids, s_w, -2, s_spec, &kth_lo);
+          QMOE_STAMP(4, 0);
         } else {
           // timed out: flag it for the host (the call's result is not
           // trustworthy), stream expert 0 tentatively and route this
@@ -764,16 +794,22 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
     while (__hip_atomic_load(&s_spec[rk], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
       __builtin_amdgcn_s_sleep(1);
   }
+  QMOE_STAMP(5, 1);
+  QMOE_STAMP(12, 7);
   te0 = run_expert(0, true);
   te1 = nruns > 1 ? run_expert(1, true) : 0;
   process_rows(te0, te1, 3, use_burst);
+  QMOE_STAMP(7, 1);
+  QMOE_STAMP(14, 7);
   if (ctl && a.fused_router) {
     // out's zeros, every workgroup's slice, before this workgroup's atomics
     if (poll_zero_flags(a.ztag, gridDim.x, a.epoch, a.xchg_ticks)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     else if (threadIdx.x == 0) __hip_atomic_store(a.xchg_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
+  QMOE_STAMP(8, 0);
   if (threadIdx.x == 0) s_exact = need_exact;
   __syncthreads();  // run sums, s_ids/s_w (when certified), s_sg, s_exact
+  QMOE_STAMP(9, 0);
   if (s_exact) {
     // certification failed: the whole block computes the exact routing
     exact_logits_block(xs, H, a.rw, a.rs, a.rfmt, a.E, lt, kFusedBlock);
@@ -828,6 +864,7 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
     if (nruns > 1) v = fmaf(w1, s1, v);
     atomicAdd(out_t + j, v);
   }
+  QMOE_STAMP_DRAINED(10, 0);
 }
 
 // Splits each token's k*I (+ Is) intermediate rows evenly over about one
@@ -947,3 +984,14 @@ hipError_t launch_expert_fused(const FusedArgs &a, hipStream_t st) {
 }
 
 }  // namespace qmoe
+
+#ifdef QMOE_TIMELINE
+// The instrumented library's read-out of the stamps: n words from the start.
+extern "C" int qmoe_timeline_read(uint64_t *host, int n) {
+  if (!host || n < 0 || n > qmoe::kMaxExchangeBlocks * qmoe::kStampsPerBlock) return 1;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(qmoe::g_timeline), (size_t)n * 8, 0, hipMemcpyDeviceToHost) ==
+                 hipSuccess
+             ? 0
+             : 4;
+}
+#endif

@@ -353,7 +353,7 @@ hipError_t launch_linear_relayout(int fmt, const uint8_t *src, const uint16_t *s
 // (no comparison against a NaN best succeeds).  Two stages: workgroups reduce
 // chunks to (value, index) pairs, one workgroup per row reduces the pairs.
 constexpr int kArgmaxThreads = 256;
-constexpr int kArgmaxChunk = 8192;  // elements per first-stage workgroup
+constexpr int kArgmaxChunk = 1024;  // elements per first-stage workgroup (about 150 for a 152k vocabulary)
 
 struct ArgPair {
   float v;

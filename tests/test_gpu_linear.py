@@ -130,7 +130,7 @@ def test_lm_head_greedy_token():
     assert list(tok) == want and tok1[0] == want[0]
 
 
-@pytest.mark.parametrize("n", [1, 7, 8192, 8193, 151936])
+@pytest.mark.parametrize("n", [1, 7, 1024, 1025, 8193, 151936])
 def test_argmax_device_semantics(n):
     import torch
     announce(f"argmax n={n} T=6 with ties and NaNs")
