@@ -264,10 +264,12 @@ int64_t qmoe_device_bytes(const qmoe_layer *layer);
  * bit for bit.  It replaces linear.matvec / mat2D / proj
  * (model/model.go:131-205) and quantLinear.forward (model/moe.go:159-162)
  * for the dense MLP projections (model.go:350-358) and the LM head
- * (model.go:519-525, tied: the embedding matrix).  Formats as above; the
- * f32-scale formats are stored as their exact f32 dequantisation.  in_dim must
- * be a multiple of 32 (f32 and the f32-scale formats), 64 (bf16) or 256
- * (int8, int4); other shapes return QMOE_ERR_UNSUPPORTED.  The device copy is
+ * (model.go:519-525, tied: the embedding matrix).  Formats as above; every
+ * group-32 format keeps its codes and its own scales (fp16, or the f32 scales
+ * of qwen-quant's projections), each weight dequantised in the kernel as
+ * float32(code) * scale exactly as quantLinear.dequantize does.  in_dim must
+ * be a multiple of 32 (f32), 64 (bf16) or 256 (the group-32 formats) and at
+ * most 40960; other shapes return QMOE_ERR_UNSUPPORTED.  The device copy is
  * rearranged at upload for the GEMV (64-row blocks; the same bytes plus
  * padding to a multiple of 64 rows).  Same threading rules as qmoe_layer. */
 typedef struct qmoe_linear qmoe_linear;

@@ -120,7 +120,7 @@ qmoe_status qmoe_linear_create(int32_t out_dim, int32_t in_dim, int32_t fmt, int
   *out = nullptr;
   if (out_dim <= 0 || in_dim <= 0) return lfail(nullptr, QMOE_ERR_INVALID, "dimensions must be positive");
   if (fmt < QMOE_F32 || fmt > QMOE_INT4G32_F32S) return lfail(nullptr, QMOE_ERR_INVALID, "unknown format");
-  const int sf = lin_f32s(fmt) ? (int)kF32 : fmt;
+  const int sf = fmt;  // every format is kept as given (group-32: codes + their scales)
   if ((fmt_quant(fmt) || lin_f32s(fmt)) && in_dim % kGroup)
     return lfail(nullptr, QMOE_ERR_INVALID, "quantised formats need in_dim % 32 == 0");
   if (!linear_supported(sf, in_dim))
@@ -185,38 +185,28 @@ qmoe_status qmoe_linear_set(qmoe_linear *l, const void *w, const void *scales) {
   const bool f32s = lin_f32s(l->fmt);
   if ((fmt_quant(l->fmt) || f32s) && !scales) return lfail(l, QMOE_ERR_INVALID, "null scale pointer");
   const LinMat &m = l->m;
-  // row blocks staged through the device in the reference layout, then
-  // rewritten into the lane stream (group-32 codes with f32 scales first
-  // dequantised exactly to f32)
-  const int bits = l->fmt == QMOE_INT8G32_F32S ? 8 : 4;
-  const int in_fmt = f32s ? (bits == 8 ? (int)kINT8 : (int)kINT4) : m.fmt;
-  const int64_t in_row = fmt_matrix_bytes(in_fmt, 1, m.cols);
-  const int64_t sc_row = (fmt_quant(in_fmt) ? (int64_t)(m.cols / kGroup) : 0) * (f32s ? 4 : 2);
-  const int64_t f32_row = f32s ? (int64_t)m.cols * 4 : 0;
-  const int64_t per = in_row + sc_row + f32_row;
+  // row blocks staged through the device in the reference layout (codes or
+  // elements, then the scales: fp16 bits, or f32 for the f32-scale formats),
+  // then rewritten into the lane stream
+  const int base = f32s ? (l->fmt == QMOE_INT8G32_F32S ? (int)kINT8 : (int)kINT4) : m.fmt;
+  const int64_t in_row = fmt_matrix_bytes(base, 1, m.cols);
+  const int64_t sc_row = (fmt_quant(base) ? (int64_t)(m.cols / kGroup) : 0) * (f32s ? 4 : 2);
+  const int64_t per = in_row + sc_row;
   int64_t chunk = std::min<int64_t>(m.rows, std::max<int64_t>(64, ((int64_t)256 << 20) / per));
   chunk = (chunk + 63) / 64 * 64;  // whole 64-row blocks of the stream
   uint8_t *tmp = nullptr;
   LHIP_TRY(l, hipMalloc(&tmp, (size_t)(chunk * per)), "hipMalloc upload staging");
-  const int64_t units_row = linear_stream_bytes(m.fmt, 64, m.cols) / 64;  // stream bytes per row
+  const int64_t stream_row = linear_stream_bytes(m.fmt, 64, m.cols) / 64;  // stream bytes per row
   qmoe_status st = QMOE_OK;
   for (int64_t r0 = 0; r0 < m.rows; r0 += chunk) {
     const int64_t n = std::min(chunk, (int64_t)m.rows - r0);
     uint8_t *tsc = tmp + n * in_row;
-    uint8_t *tf = tsc + n * sc_row;
     hipError_t e = hipMemcpy(tmp, (const uint8_t *)w + r0 * in_row, (size_t)(n * in_row), hipMemcpyHostToDevice);
     if (e == hipSuccess && sc_row)
       e = hipMemcpy(tsc, (const uint8_t *)scales + r0 * sc_row, (size_t)(n * sc_row), hipMemcpyHostToDevice);
-    const uint8_t *src = tmp;
-    const uint16_t *ss = (const uint16_t *)tsc;
-    if (e == hipSuccess && f32s) {
-      e = launch_dequant_f32s(bits, tmp, reinterpret_cast<const float *>(tsc), n, m.cols,
-                              reinterpret_cast<float *>(tf), l->stream);
-      src = tf;
-      ss = nullptr;
-    }
     if (e == hipSuccess)
-      e = launch_linear_relayout(m.fmt, src, ss, (int)n, m.cols, (uint8_t *)l->wbuf + r0 * units_row, l->stream);
+      e = launch_linear_relayout(m.fmt, tmp, sc_row ? tsc : nullptr, (int)n, m.cols,
+                                 (uint8_t *)l->wbuf + r0 * stream_row, l->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
     if (e != hipSuccess) {
       st = lhip(l, e, "weight upload");

@@ -221,16 +221,21 @@ hipError_t launch_relayout_transpose(int fmt, const uint8_t *src, const uint16_t
 // linear.matvec / matmulVec / quantLinear.forward (model/model.go:131-176,
 // model/tensors.go:77-89, model/moe.go:159-162).  W is held in the lane-stream
 // layout that launch_linear_relayout writes (linear_stream_bytes bytes).
+// The GEMV's formats: the Fmt values plus the group-32 formats with f32
+// scales (the qmoe_format numbers QMOE_INT8G32_F32S / QMOE_INT4G32_F32S),
+// kept as codes + f32 scales.
+constexpr int kLinI8F32S = 4, kLinI4F32S = 5;
 struct LinMat {
   const uint8_t *w = nullptr;
   int fmt = 0, rows = 0, cols = 0;
   int n_cu = 256;  // compute units of the device (launch shape)
 };
-int linear_step(int fmt);  // cols must be a multiple of it (32 f32, 64 bf16, 256 int8/int4)
+int linear_step(int fmt);  // cols must be a multiple of it (32 f32, 64 bf16, 256 for the group-32 formats)
 bool linear_supported(int fmt, int cols);  // also cols <= 40960 (x of a token in LDS)
 int linear_tokens_per_pass(int T, int cols);  // a launch covers T in passes of this many tokens
 int64_t linear_stream_bytes(int fmt, int rows, int cols);
-hipError_t launch_linear_relayout(int fmt, const uint8_t *src, const uint16_t *ss, int rows, int cols, void *dst,
+// ss: fp16 scale bits (int8/int4) or f32 scales (the f32-scale formats), (rows, cols / 32)
+hipError_t launch_linear_relayout(int fmt, const uint8_t *src, const void *ss, int rows, int cols, void *dst,
                                   hipStream_t st);
 hipError_t launch_linear(const float *x, int T, const LinMat &m, float *y, hipStream_t st);
 // argmax of each row of v (T, n) with model.go:652-660's semantics; pv/pi

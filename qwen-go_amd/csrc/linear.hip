@@ -27,18 +27,24 @@ namespace qmoe {
 constexpr int kLinMaxTok = 8;  // tokens per pass
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Lane-stream geometry of a format: units per super-chunk (SCU), elements per
-// super-chunk, and whether the first unit is the scale vector.
-template <int FMT>
+// Lane-stream geometry of a format (the qmoe_format numbers: f32, bf16,
+// int8 / int4 group-32 with fp16 scales, int8 / int4 group-32 with f32
+// scales): units per super-chunk (SCU), elements per super-chunk; for the
+// group-32 formats the super-chunk's 8 scales come first, in one unit (fp16)
+// or two (f32).
+template <int LF>
 struct LinFmt {
-  static constexpr bool kQuant = FMT == kINT8 || FMT == kINT4;
-  static constexpr int kCodeUnits = FMT == kINT8 ? 16 : 8;            // 16-byte units of codes / elements
-  static constexpr int kUnits = kCodeUnits + (kQuant ? 1 : 0);         // SCU
-  static constexpr int kElems = kCodeUnits * Chunk<FMT>::kElems;       // 32 f32, 64 bf16, 256 int8/int4
-  static constexpr int kRing = fmt_quant(FMT) ? 1 : 2;                // super-chunks in flight
+  static constexpr int kBase = LF == kLinI8F32S ? kINT8 : LF == kLinI4F32S ? kINT4 : LF;  // code / element type
+  static constexpr int kScaleBytes = (LF == kINT8 || LF == kINT4) ? 2 : (LF == kLinI8F32S || LF == kLinI4F32S) ? 4 : 0;
+  static constexpr bool kQuant = kScaleBytes > 0;
+  static constexpr int kScaleUnits = kScaleBytes * 8 / 16;
+  static constexpr int kCodeUnits = kBase == kINT8 ? 16 : 8;          // 16-byte units of codes / elements
+  static constexpr int kUnits = kCodeUnits + kScaleUnits;              // SCU
+  static constexpr int kElems = kCodeUnits * Chunk<kBase>::kElems;     // 32 f32, 64 bf16, 256 int8/int4
+  static constexpr int kRing = kQuant ? 1 : 2;                         // super-chunks in flight
   // deeper ring for launches of at most one wave per SIMD, where the few waves
   // are bound by the latency of their own loads
-  static constexpr int kDeepRing = FMT == kINT8 ? 2 : FMT == kINT4 ? 4 : 6;
+  static constexpr int kDeepRing = kBase == kINT8 ? 2 : kBase == kINT4 ? 4 : 6;
 };
 
 int linear_step(int fmt) {
@@ -47,6 +53,8 @@ int linear_step(int fmt) {
   case kBF16: return LinFmt<kBF16>::kElems;
   case kINT8: return LinFmt<kINT8>::kElems;
   case kINT4: return LinFmt<kINT4>::kElems;
+  case kLinI8F32S: return LinFmt<kLinI8F32S>::kElems;
+  case kLinI4F32S: return LinFmt<kLinI4F32S>::kElems;
   default: return 0;
   }
 }
@@ -64,7 +72,9 @@ int64_t linear_units_per_row(int fmt, int cols) {
   case kF32: return cols / LinFmt<kF32>::kElems * LinFmt<kF32>::kUnits;
   case kBF16: return cols / LinFmt<kBF16>::kElems * LinFmt<kBF16>::kUnits;
   case kINT8: return cols / LinFmt<kINT8>::kElems * LinFmt<kINT8>::kUnits;
-  default: return cols / LinFmt<kINT4>::kElems * LinFmt<kINT4>::kUnits;
+  case kINT4: return cols / LinFmt<kINT4>::kElems * LinFmt<kINT4>::kUnits;
+  case kLinI8F32S: return cols / LinFmt<kLinI8F32S>::kElems * LinFmt<kLinI8F32S>::kUnits;
+  default: return cols / LinFmt<kLinI4F32S>::kElems * LinFmt<kLinI4F32S>::kUnits;
   }
 }
 
@@ -144,14 +154,15 @@ constexpr bool kLinLookahead = TT * Chunk<FMT>::kElems <= 16;
 // the register only after the sum keeps each slot in one register across
 // iterations: no copies, which would wait for every load in flight.  A
 // scheduling barrier closes every unit, so the loads stay in ring order.
-template <int FMT, int TT, int R, bool RELOAD>
-__device__ __forceinline__ void lin_super(u32x4 (&b)[LinFmt<FMT>::kUnits], const u32x4 *__restrict__ p, int c,
-                                          const float *const *xt, int cols, LinX<FMT, TT> &xc,
+template <int LF, int TT, int R, bool RELOAD>
+__device__ __forceinline__ void lin_super(u32x4 (&b)[LinFmt<LF>::kUnits], const u32x4 *__restrict__ p, int c,
+                                          const float *const *xt, int cols, LinX<LinFmt<LF>::kBase, TT> &xc,
                                           float (&acc)[TT]) {
 #pragma clang fp contract(off)
-  using F = LinFmt<FMT>;
+  using F = LinFmt<LF>;
+  constexpr int FMT = F::kBase;
   constexpr int SCU = F::kUnits, EPC = Chunk<FMT>::kElems;
-  constexpr int U0 = F::kQuant ? 1 : 0;
+  constexpr int U0 = F::kScaleUnits;
   constexpr bool LA = kLinLookahead<FMT, TT>;
   const u32x4 *nx = p + (size_t)((c + R) * SCU) * 64;
 #pragma unroll
@@ -161,8 +172,11 @@ __device__ __forceinline__ void lin_super(u32x4 (&b)[LinFmt<FMT>::kUnits], const
     if constexpr (LA) lin_read_x<FMT, TT>(xn, xt, min(k + EPC, cols - EPC));  // next unit (the last re-reads itself)
     else lin_read_x<FMT, TT>(xc, xt, k);
     float s = 0.0f;
-    if constexpr (FMT == kINT8) s = half_of(b[0], u >> 1);
-    if constexpr (FMT == kINT4) s = half_of(b[0], u);
+    if constexpr (F::kQuant) {
+      const int g = FMT == kINT8 ? u >> 1 : u;  // the unit's group of 32 elements
+      if constexpr (F::kScaleBytes == 2) s = half_of(b[0], g);
+      else s = __uint_as_float(b[g >> 2][g & 3]);
+    }
     u32x4 v = b[U0 + u];
     // int8: opaque here, or the compiler splits the loads into bytes at the
     // load and holds 4x the registers across the ring
@@ -177,15 +191,19 @@ __device__ __forceinline__ void lin_super(u32x4 (&b)[LinFmt<FMT>::kUnits], const
     if constexpr (LA) xc = xn;
     __builtin_amdgcn_sched_barrier(0);
   }
-  if constexpr (F::kQuant && RELOAD) b[0] = __builtin_nontemporal_load(nx);
+  if constexpr (RELOAD) {
+#pragma unroll
+    for (int q = 0; q < F::kScaleUnits; q++) b[q] = __builtin_nontemporal_load(nx + (size_t)q * 64);
+  }
 }
 
-template <int FMT, int TT, int R>
+template <int LF, int TT, int R>
 __global__ void __launch_bounds__(256) linear_stream_kernel(const float *__restrict__ x, int T, int cols,
                                                             const u32x4 *__restrict__ w, int rows,
                                                             float *__restrict__ y) {
 #pragma clang fp contract(off)
-  using F = LinFmt<FMT>;
+  using F = LinFmt<LF>;
+  constexpr int FMT = F::kBase;
   constexpr int SCU = F::kUnits;
   extern __shared__ __align__(16) float xs[];  // this workgroup's tokens of x, (nt, cols)
   const int t0 = blockIdx.y * TT;
@@ -224,19 +242,19 @@ __global__ void __launch_bounds__(256) linear_stream_kernel(const float *__restr
 #pragma nounroll
   for (; c + 2 * R <= nsc; c += R) {
 #pragma unroll
-    for (int r = 0; r < R; r++) lin_super<FMT, TT, R, true>(buf[r], p, c + r, xt, cols, xc, acc);
+    for (int r = 0; r < R; r++) lin_super<LF, TT, R, true>(buf[r], p, c + r, xt, cols, xc, acc);
   }
   // the last fewer than 2R super-chunks
 #pragma unroll
   for (int r = 0; r < R; r++) {
     if (c + r < nsc) {
-      if (c + r + R < nsc) lin_super<FMT, TT, R, true>(buf[r], p, c + r, xt, cols, xc, acc);
-      else lin_super<FMT, TT, R, false>(buf[r], p, c + r, xt, cols, xc, acc);
+      if (c + r + R < nsc) lin_super<LF, TT, R, true>(buf[r], p, c + r, xt, cols, xc, acc);
+      else lin_super<LF, TT, R, false>(buf[r], p, c + r, xt, cols, xc, acc);
     }
   }
 #pragma unroll
   for (int r = 0; r < R; r++)
-    if (c + R + r < nsc) lin_super<FMT, TT, R, false>(buf[r], p, c + R + r, xt, cols, xc, acc);
+    if (c + R + r < nsc) lin_super<LF, TT, R, false>(buf[r], p, c + R + r, xt, cols, xc, acc);
   const int row = blk * 64 + lane;
   if (row < rows) {
 #pragma unroll
@@ -294,16 +312,19 @@ hipError_t launch_linear(const float *x, int T, const LinMat &m, float *y, hipSt
   case kF32: return linear_launch_fmt<kF32>(x, T, m, y, st);
   case kBF16: return linear_launch_fmt<kBF16>(x, T, m, y, st);
   case kINT8: return linear_launch_fmt<kINT8>(x, T, m, y, st);
-  default: return linear_launch_fmt<kINT4>(x, T, m, y, st);
+  case kINT4: return linear_launch_fmt<kINT4>(x, T, m, y, st);
+  case kLinI8F32S: return linear_launch_fmt<kLinI8F32S>(x, T, m, y, st);
+  default: return linear_launch_fmt<kLinI4F32S>(x, T, m, y, st);
   }
 }
 
-// ---- relayout: row-major (rows, cols) codes / elements (+ fp16 scales) into
-// the lane stream.  One thread per (unit, lane); rows past the end are zeros.
-template <int FMT>
-__global__ void linear_relayout_kernel(const uint8_t *__restrict__ src, const uint16_t *__restrict__ ss, int rows,
+// ---- relayout: row-major (rows, cols) codes / elements (+ their fp16 or f32
+// scales, (rows, cols / 32)) into the lane stream.  One thread per (unit,
+// lane); rows past the end are zeros.
+template <int LF>
+__global__ void linear_relayout_kernel(const uint8_t *__restrict__ src, const void *__restrict__ ss, int rows,
                                        int cols, u32x4 *__restrict__ dst, int64_t total) {
-  using F = LinFmt<FMT>;
+  using F = LinFmt<LF>;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int lane = (int)(i & 63);
@@ -316,33 +337,42 @@ __global__ void linear_relayout_kernel(const uint8_t *__restrict__ src, const ui
   const int64_t row = blk * 64 + lane;
   u32x4 v = {0u, 0u, 0u, 0u};
   if (row < rows) {
-    const int64_t row_bytes = fmt_matrix_bytes(FMT, 1, cols);
-    if (F::kQuant && u == 0) {
-      const uint16_t *sr = ss + row * (cols / kGroup) + sc * 8;
-      uint32_t h[4];
+    const int64_t row_bytes = fmt_matrix_bytes(F::kBase, 1, cols);
+    if (u < F::kScaleUnits) {
+      if constexpr (F::kScaleBytes == 2) {
+        const uint16_t *sr = static_cast<const uint16_t *>(ss) + row * (cols / kGroup) + sc * 8;
+        uint32_t h[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) h[j] = (uint32_t)sr[2 * j] | ((uint32_t)sr[2 * j + 1] << 16);
-      v = u32x4{h[0], h[1], h[2], h[3]};
+        for (int j = 0; j < 4; j++) h[j] = (uint32_t)sr[2 * j] | ((uint32_t)sr[2 * j + 1] << 16);
+        v = u32x4{h[0], h[1], h[2], h[3]};
+      } else if constexpr (F::kScaleBytes == 4) {
+        const uint32_t *sr = static_cast<const uint32_t *>(ss) + row * (cols / kGroup) + sc * 8 + u * 4;
+        v = u32x4{sr[0], sr[1], sr[2], sr[3]};
+      }
     } else {
-      const int cu = u - (F::kQuant ? 1 : 0);
+      const int cu = u - F::kScaleUnits;
       v = *reinterpret_cast<const u32x4 *>(src + row * row_bytes + (int64_t)sc * F::kCodeUnits * 16 + cu * 16);
     }
   }
   dst[i] = v;
 }
 
-hipError_t launch_linear_relayout(int fmt, const uint8_t *src, const uint16_t *ss, int rows, int cols, void *dst,
+hipError_t launch_linear_relayout(int fmt, const uint8_t *src, const void *ss, int rows, int cols, void *dst,
                                   hipStream_t st) {
   if (!linear_supported(fmt, cols)) return hipErrorInvalidValue;
   const int64_t total = linear_stream_bytes(fmt, rows, cols) / 16;
   const dim3 grid((unsigned)((total + 255) / 256));
   u32x4 *d = reinterpret_cast<u32x4 *>(dst);
+#define RL(LF) hipLaunchKernelGGL(linear_relayout_kernel<LF>, grid, dim3(256), 0, st, src, ss, rows, cols, d, total)
   switch (fmt) {
-  case kF32: hipLaunchKernelGGL(linear_relayout_kernel<kF32>, grid, dim3(256), 0, st, src, ss, rows, cols, d, total); break;
-  case kBF16: hipLaunchKernelGGL(linear_relayout_kernel<kBF16>, grid, dim3(256), 0, st, src, ss, rows, cols, d, total); break;
-  case kINT8: hipLaunchKernelGGL(linear_relayout_kernel<kINT8>, grid, dim3(256), 0, st, src, ss, rows, cols, d, total); break;
-  default: hipLaunchKernelGGL(linear_relayout_kernel<kINT4>, grid, dim3(256), 0, st, src, ss, rows, cols, d, total); break;
+  case kF32: RL(kF32); break;
+  case kBF16: RL(kBF16); break;
+  case kINT8: RL(kINT8); break;
+  case kINT4: RL(kINT4); break;
+  case kLinI8F32S: RL(kLinI8F32S); break;
+  default: RL(kLinI4F32S); break;
   }
+#undef RL
   return hipGetLastError();
 }
 

@@ -402,8 +402,9 @@ class Linear:
 
 
 def linear_step(fmt: int) -> int:
-    """in_dim granularity of Linear (the f32-scale formats are stored as f32)."""
-    return {F32: 32, BF16: 64, INT8G32: 256, INT4G32: 256, INT8G32_F32S: 32, INT4G32_F32S: 32}[fmt]
+    """in_dim granularity of Linear: one super-chunk of a row (256 elements for
+    every group-32 format, whose 8 scales travel with it)."""
+    return {F32: 32, BF16: 64, INT8G32: 256, INT4G32: 256, INT8G32_F32S: 256, INT4G32_F32S: 256}[fmt]
 
 
 def quantize_device(bits: int, d_w: int, n_mat: int, rows: int, cols: int, d_codes: int,

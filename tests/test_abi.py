@@ -126,6 +126,7 @@ def test_synthetic_weights_are_seeded():
     (16, 160, qmoe.INT4G32, 5),          # int4 and int8 super-chunks are 256 elements
     (16, 384, qmoe.INT8G32, 5),
     (16, 48, qmoe.INT8G32_F32S, 1),
+    (16, 96, qmoe.INT4G32_F32S, 5),           # f32-scale formats keep their codes: 256-element steps
 ])
 def test_linear_create_rejects_bad_shapes(out_dim, in_dim, fmt, status):
     lib = qmoe.load_library()

@@ -46,7 +46,8 @@ CASES = [  # (fmt, rows, cols, T)
     (qmoe.INT8G32, 777, 2048, 1), (qmoe.INT8G32, 130, 256, 9), (qmoe.INT8G32, 64, 768, 2),
     (qmoe.INT4G32, 1500, 2048, 1), (qmoe.INT4G32, 65, 256, 3), (qmoe.INT4G32, 2048, 512, 1),
     (qmoe.BF16, 100, 4096, 4), (qmoe.BF16, 2048, 768, 1), (qmoe.F32, 129, 96, 8),
-    (qmoe.INT8G32_F32S, 512, 2048, 1), (qmoe.INT4G32_F32S, 300, 1024, 4),
+    (qmoe.INT8G32_F32S, 512, 2048, 1), (qmoe.INT4G32_F32S, 300, 1024, 4), (qmoe.INT8G32_F32S, 70, 768, 9),
+    (qmoe.INT4G32_F32S, 4096, 2048, 1),
 ]
 
 
