@@ -128,6 +128,11 @@ qmoe_status qmoe_quantize_device(int32_t bits, const float *d_w, int64_t n_mat, 
  * receive the selected experts and renormalised routing weights in rank
  * order; either may be NULL.  T == 0 is a no-op.  The Go seam calls it with
  * T = 1 (model/model.go:508-514).
+ * Precision: ids are the reference's exactly; the routing weights are within
+ * 1e-4 relative of the reference's f32 softmax on the decode path (T <= 32:
+ * computed from the certified f64 partial sums) and within 1e-6 on the
+ * batched path (the reference's f32 softmax of the exact logits); out is
+ * within 1e-3 (decode) / 2e-2 (batched, bf16 matrix cores) normwise per token.
  * At T = 1 the expert kernel's workgroups exchange the router partials among
  * themselves; if that exchange times out (the device did not run them all at
  * once) this call returns QMOE_ERR_HIP and its outputs are not valid. */
@@ -254,6 +259,13 @@ qmoe_status qmoe_router_rescues(qmoe_layer *layer, int64_t *count);
  * QMOE_ERR_HIP, and every workgroup still finishes (on exact routing).  For
  * tests of that error path. */
 qmoe_status qmoe_debug_exchange_budget(qmoe_layer *layer, int64_t ticks);
+
+/* No counterpart in the reference: sizes the handle's workspace for calls of
+ * up to max_T tokens now (longer prompts run in chunks of at most
+ * 65535 / top_k tokens, so larger values are capped there), so that no later
+ * call allocates device memory -- e.g. at load, with the longest prompt a
+ * server accepts.  Calls with more tokens still grow it. */
+qmoe_status qmoe_reserve(qmoe_layer *layer, int32_t max_T);
 
 /* Bytes of device memory held by the handle (weights + workspace). */
 int64_t qmoe_device_bytes(const qmoe_layer *layer);

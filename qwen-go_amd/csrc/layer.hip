@@ -1265,6 +1265,18 @@ qmoe_status qmoe_debug_exchange_budget(qmoe_layer *l, int64_t ticks) {
   return QMOE_OK;
 }
 
+qmoe_status qmoe_reserve(qmoe_layer *l, int32_t max_T) {
+  if (!l) return QMOE_ERR_INVALID;
+  std::lock_guard<std::mutex> g(l->mu);
+  qmoe_status s = enter(l);
+  if (s) return s;
+  if (max_T < 0) return fail(l, QMOE_ERR_INVALID, "max_T < 0");
+  if (max_T == 0) return QMOE_OK;
+  // the batched path's buffers are sized when that path is taken; a T that
+  // takes it sizes them now (weights must be uploaded for the path choice)
+  return ensure_workspace(l, std::min<int>(max_T, chunk_tokens(l)), nullptr);
+}
+
 int64_t qmoe_device_bytes(const qmoe_layer *l) {
   if (!l) return 0;
   return l->weight_bytes + (int64_t)l->ws.n;

@@ -78,6 +78,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "qmoe_debug_exchange_budget": ([vp, i64], i32),
         "qmoe_forward_device_noalloc": ([vp, vp, i32, vp, vp, vp, vp], i32),
         "qmoe_set_post_norm": ([vp, vp, ctypes.c_float], i32),
+        "qmoe_reserve": ([vp, i32], i32),
         "qmoe_forward_residual": ([vp, vp, i32, vp, vp], i32),
         "qmoe_forward_residual_device": ([vp, vp, i32, vp, vp, vp, vp], i32),
         "qmoe_norm_recomputes": ([vp, vp], i32),
@@ -107,7 +108,7 @@ def exported_symbols() -> list[str]:
             "qmoe_quantize_device", "qmoe_forward", "qmoe_forward_device", "qmoe_dequant_debug",
             "qmoe_device_bytes", "qmoe_profile_enable", "qmoe_profile_read", "qmoe_router_fallbacks",
             "qmoe_router_rescues", "qmoe_router_bounds_debug", "qmoe_debug_exchange_budget",
-            "qmoe_forward_device_noalloc", "qmoe_set_post_norm", "qmoe_forward_residual",
+            "qmoe_forward_device_noalloc", "qmoe_reserve", "qmoe_set_post_norm", "qmoe_forward_residual",
             "qmoe_forward_residual_device", "qmoe_norm_recomputes", "qmoe_debug_norm_sequential", "qmoe_norm_debug",
             "qmoe_linear_create", "qmoe_linear_destroy", "qmoe_linear_last_error", "qmoe_linear_set",
             "qmoe_linear_forward", "qmoe_linear_forward_device", "qmoe_linear_greedy",
@@ -239,6 +240,10 @@ class MoeLayer:
         """forward_device for T <= 32 with no device allocation (the kernels'
         scratch is a static device array shared by every call on the device)."""
         self._check(self.lib.qmoe_forward_device_noalloc(self.h, d_x, T, d_out, d_ids, d_w, stream))
+
+    def reserve(self, max_T: int) -> None:
+        """Size the workspace for calls of up to max_T tokens now (no allocation later)."""
+        self._check(self.lib.qmoe_reserve(self.h, max_T))
 
     def set_post_norm(self, w, eps: float):
         """postAttentionLayernorm (H) f32 and float32(RmsNormEps)."""

@@ -763,3 +763,27 @@ def test_contract_errors():
     finally:
         layer.close()
     layer.close()  # idempotent
+
+
+def test_reserve_sizes_the_workspace_up_front():
+    """qmoe_reserve(max_T): later calls of up to max_T tokens allocate nothing
+    (the handle's device bytes stay put) and still match the oracle."""
+    cfg = qmoe.LayerConfig(256, 16, 4, 128, 64, 16, qmoe.BF16, qmoe.BF16, qmoe.BF16, "reserve")
+    announce("reserve T=300 then forwards of T=1, 40, 300")
+    hw = qmoe.synthetic_weights(cfg, 61, quantizer=oracle.host_quantizer)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        before = layer.device_bytes()
+        layer.reserve(300)
+        reserved = layer.device_bytes()
+        assert reserved > before
+        for T in (1, 40, 300):
+            x = qmoe.synthetic_tokens(cfg, T, 61 + T)
+            out, ids, _ = layer.forward(x)
+            assert layer.device_bytes() == reserved
+            ref, rids, _ = oracle.OracleLayer(hw).forward(x)
+            assert np.array_equal(ids, rids)
+            assert rel_err(out, ref) <= path_tol(layer, T)
+    finally:
+        layer.close()
