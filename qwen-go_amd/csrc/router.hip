@@ -182,13 +182,18 @@ static hipError_t router_logits_fmt(const float *x, int T, const DevMat &r, floa
     QMOE_LAUNCH(router_rowwise_kernel<FMT>, grid, dim3(64), (size_t)H * sizeof(float), st, x,
                        T, H, r.w, r.s, E, logits);
   } else {
-    // 2x2 outputs per lane while that still fills 256 CUs four waves deep,
-    // else one output per lane and four times the workgroups
-    const bool wide = (int64_t)T * E >= (int64_t)4 * 256 * 256;
-    const dim3 b(256), g11((E + 15) / 16, (T + 15) / 16), g22((E + 31) / 32, (T + 31) / 32);
+    // two experts of one token per lane (two waves per SIMD at T x E = 2^18:
+    // C3 router 64 -> 50 us against 2x2 outputs per lane at one wave per
+    // SIMD, 54 us at one output per lane); 2x2 per lane only once that still
+    // gives every CU four workgroups
+    const bool wide = (int64_t)T * E >= (int64_t)16 * 256 * 256;
+    const dim3 b(256), g11((E + 15) / 16, (T + 15) / 16), g22((E + 31) / 32, (T + 31) / 32),
+        g12((E + 31) / 32, (T + 15) / 16);
     if (H % 64 == 0) {
       if (wide)
         QMOE_LAUNCH((router_tiled_kernel<FMT, 2, 2, 64>), g22, b, 0, st, x, T, H, r.w, r.s, E, logits);
+      else if (E >= 32)
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 2, 64>), g12, b, 0, st, x, T, H, r.w, r.s, E, logits);
       else
         QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 1, 64>), g11, b, 0, st, x, T, H, r.w, r.s, E, logits);
     } else {
