@@ -293,14 +293,21 @@ def test_decode_router_exchange_many_calls(fmts):
     assert err <= TOL_F32, f"normwise relative error {err:.3e} > {TOL_F32}"
 
 
-@pytest.mark.parametrize("rf,H,T", [(qmoe.F32, 288, 40), (qmoe.INT8G32, 288, 40), (qmoe.INT4G32, 288, 2100),
-                                     (qmoe.BF16, 320, 2100), (qmoe.BF16, 288, 2100)])
-def test_router_tile_shapes(rf, H, T):
-    """The exact router for T > 32 in each of its tilings: one output per lane
-    (T=40) and four (T=2100 x 128 experts), with 64-wide k slices (H=320) and
-    32-wide ones (H=288).  ids must equal the reference's exactly."""
-    cfg = qmoe.LayerConfig(H, 128, 8, 64, 0, 128, rf, qmoe.BF16, qmoe.BF16, "router-tiles")
-    announce(f"router tiles fmt={rf} H={H} T={T}")
+@pytest.mark.parametrize("rf,H,T,E", [(qmoe.F32, 288, 40, 128), (qmoe.INT8G32, 288, 40, 128),
+                                       (qmoe.INT4G32, 288, 2100, 128), (qmoe.BF16, 320, 2100, 128),
+                                       (qmoe.BF16, 288, 2100, 128), (qmoe.F32, 256, 70, 40),
+                                       (qmoe.INT8G32, 512, 300, 72), (qmoe.BF16, 2048, 33, 128),
+                                       (qmoe.INT4G32, 1024, 129, 24), (qmoe.INT8G32, 256, 8200, 128),
+                                       (qmoe.INT4G32, 288, 8200, 128)])
+def test_router_tile_shapes(rf, H, T, E):
+    """The exact router for T > 32 in each of its tilings: 64-wide k slices
+    (H a multiple of 64) with one output per lane below 32 experts (E=24), two
+    below T x E = 2^20 (tails in T and E: T=70, E=40; T=300, E=72) and four
+    from there (T=8200 x 128 experts, an int8 router: a bf16 one takes the
+    certified path there); 32-wide slices (H=288) with one output per lane
+    (T=40, 2100) or four (T=8200).  ids must equal the reference's exactly."""
+    cfg = qmoe.LayerConfig(H, E, 8, 64, 0, E, rf, qmoe.BF16, qmoe.BF16, "router-tiles")
+    announce(f"router tiles fmt={rf} H={H} T={T} E={E}")
     hw = qmoe.synthetic_weights(cfg, 7 + T, quantizer=oracle.host_quantizer)
     x = qmoe.synthetic_tokens(cfg, T, 7 + T)
     check_layer(cfg, hw, x)
