@@ -491,7 +491,12 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
   const int wm = w >> 1, wn = w & 1, hi = lane >> 5, l32 = lane & 31;
   // live 32-slot blocks of this wave
   const int nrb = min(G::kNRB, max(0, (ti.rows - wm * G::kRB + 31) >> 5));
-  f32x16_t acc[G::kNRB][4];  // [slot block][gate 0, gate 1, up 0, up 1 -- or 4 column blocks]
+  // [slot block][gate 0, gate 1, up 0, up 1 -- or 4 column blocks].  The
+  // weight fragment is the MFMA's first operand, so each accumulator holds the
+  // transposed 32 x 32 block: lane l has slot l % 32 of the block and element
+  // 4 j + i column 8 j + 4 (l / 32) + i -- four consecutive columns per quad,
+  // stored as one 8-byte piece in the epilogue.
+  f32x16_t acc[G::kNRB][4];
 #pragma unroll
   for (int b = 0; b < G::kNRB; b++)
 #pragma unroll
@@ -541,7 +546,7 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
           if (b < nrb)
 #pragma unroll
             for (int q = 0; q < 4; q++)
-              acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[b][ks], bv[q][ks], acc[b][q], 0, 0, 0);
+              acc[b][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bv[q][ks], av[b][ks], acc[b][q], 0, 0, 0);
     }
   };
   if constexpr (G::kQuant) {
@@ -602,38 +607,47 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
   if constexpr (KIND == kGateUp) {
     // act = silu(g) * u -> bf16 (model/moe.go:64-75), row pitch Imax
 #pragma unroll
-    for (int b = 0; b < G::kNRB; b++)
+    for (int b = 0; b < G::kNRB; b++) {
+      const int m = wm * G::kRB + b * 32 + l32;
+      if (m < ti.rows) {
+        uint16_t *dst = a.act + (size_t)(ti.slot0 + m) * a.Imax + n0 + wn * 64 + 4 * hi;
 #pragma unroll
-      for (int j4 = 0; j4 < 4; j4++)
+        for (int q = 0; q < 2; q++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int m = wm * G::kRB + b * 32 + 8 * j4 + 4 * hi + i;
-          if (m < ti.rows) {
+          for (int j4 = 0; j4 < 4; j4++) {
+            uint16_t h[4];
 #pragma unroll
-            for (int q = 0; q < 2; q++) {
+            for (int i = 0; i < 4; i++) {
               const float g = acc[b][q][4 * j4 + i], u = acc[b][q + 2][4 * j4 + i];
               const float sgl = g / (1.0f + __expf(-g));
-              a.act[(size_t)(ti.slot0 + m) * a.Imax + n0 + wn * 64 + q * 32 + l32] = f32_to_bf16_rne(sgl * u);
+              h[i] = f32_to_bf16_rne(sgl * u);
             }
+            *reinterpret_cast<uint2 *>(dst + q * 32 + 8 * j4) =
+                make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
           }
-        }
+      }
+    }
   } else {
-    // y[slot] = routing weight (or shared gate) * (down . act), f32
+    // y[slot] = routing weight (or shared gate) * (down . act), stored bf16
 #pragma unroll
-    for (int b = 0; b < G::kNRB; b++)
+    for (int b = 0; b < G::kNRB; b++) {
+      const int m = wm * G::kRB + b * 32 + l32;
+      if (m < ti.rows) {
+        const int slot = ti.slot0 + m;
+        const float ws = a.p.wslot[slot];
+        uint16_t *dst = a.y + (size_t)slot * H + n0 + wn * 128 + 4 * hi;
 #pragma unroll
-      for (int j4 = 0; j4 < 4; j4++)
+        for (int q = 0; q < 4; q++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int m = wm * G::kRB + b * 32 + 8 * j4 + 4 * hi + i;
-          if (m < ti.rows) {
-            const int slot = ti.slot0 + m;
-            const float ws = a.p.wslot[slot];
+          for (int j4 = 0; j4 < 4; j4++) {
+            uint16_t h[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-              a.y[(size_t)slot * H + n0 + wn * 128 + q * 32 + l32] = f32_to_bf16_rne(ws * acc[b][q][4 * j4 + i]);
+            for (int i = 0; i < 4; i++) h[i] = f32_to_bf16_rne(ws * acc[b][q][4 * j4 + i]);
+            *reinterpret_cast<uint2 *>(dst + q * 32 + 8 * j4) =
+                make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
           }
-        }
+      }
+    }
   }
 }
 
