@@ -175,6 +175,7 @@ struct PrefillArgs {
   int bm;                       // slots per routed tile, prefill_tile_slots(fmt)
   int sfmt;                     // the shared expert's batched format, prefill_shared_fmt
   int bms;                      // slots per shared tile, prefill_tile_slots(sfmt)
+  int n_cu;                     // compute units of the device (8 XCDs)
   uint16_t *xb;                 // (T, H) x in bf16
   PrefillPlan p;
   const uint8_t *gu, *dn;       // gate_up (E, 2I, H); down in the reference layout (E, H, I)

@@ -566,6 +566,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     pa.bm = prefill_tile_slots(l->gu.fmt);
     pa.sfmt = Is > 0 ? l->sdownr.fmt : pa.fmt;
     pa.bms = prefill_tile_slots(pa.sfmt);
+    pa.n_cu = l->n_cu;
     pa.xb = ws.xb;
     pa.p = ws.plan;
     pa.gu = l->gu.w;

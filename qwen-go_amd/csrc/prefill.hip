@@ -363,6 +363,14 @@ __device__ __forceinline__ void dma4(const void *src, const unsigned char *lds_w
 // expert are adjacent, so an expert's B rows come from HBM about once into that
 // XCD's L2 -- and the ny column chunks of a tile back to back, which share the
 // tile's A rows in the same L2.
+//
+// A workgroup holds a CU (its LDS), so an XCD runs its n items in rounds of
+// cus = n_cu / 8.  For a bf16 gate_up, a last round of at most cus / 2 items
+// runs as twice as many half items: slots [0, 128) and [128, 256) of the tile
+// in two workgroups, each with only waves 0-3 (the first ping-pong group)
+// issuing MFMAs, which takes about 0.67 of a full item's time (C = k, T = 2048
+// at Qwen3-30B: 48 items per XCD as 32 full + 32 halves instead of two full
+// rounds).
 constexpr int kXcds = 8;
 
 template <int KIND, int BF>
@@ -376,9 +384,25 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
   const int xcd = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
   const int nt = shared_launch ? a.p.n_tiles[1] : a.p.n_tiles[0];
   const int per_xcd = (nt + kXcds - 1) / kXcds;
-  const int local = j / ny, chunk = j % ny;
-  if (local >= per_xcd) return;
-  const TileInfo ti = tile_of(a.p, a.E, shared_launch, xcd * per_xcd + local, G::kBM);
+  const int n = per_xcd * ny;  // items of this XCD
+  int split_from = n;          // items from here on run as two half items
+  if constexpr (BF == kBF16 && KIND == kGateUp) {
+    const int cus = a.n_cu / kXcds, rem = cus > 0 ? n % cus : 0;
+    if (rem > 0 && 2 * rem <= cus) split_from = n - rem;
+  }
+  int item = j, half = -1;
+  if (j >= split_from) {
+    item = split_from + (j - split_from) / 2;
+    half = (j - split_from) % 2;
+  }
+  if (item >= n) return;
+  const int chunk = item % ny;
+  TileInfo ti = tile_of(a.p, a.E, shared_launch, xcd * per_xcd + item / ny, G::kBM);
+  if (half >= 0) {
+    ti.slot0 += half * (G::kBM / 2);
+    ti.rows = min(G::kBM / 2, ti.rows - half * (G::kBM / 2));
+    ti.ok = ti.ok && ti.rows > 0;
+  }
   if (!ti.ok) return;
   const bool sh = ti.g == a.E;
   const int H = a.H;
@@ -727,7 +751,9 @@ static hipError_t gemm_launch(const PrefillArgs &a, bool shared, int ny, hipStre
   // the shared expert's GEMMs run in its own format, on tiles of its own size
   const int fmt = shared ? a.sfmt : a.fmt, bm = shared ? a.bms : a.bm;
   const int tiles = shared ? (a.T + bm - 1) / bm : prefill_max_tiles(a.T, a.k, a.E, bm);
-  const int blocks = (tiles + kXcds - 1) / kXcds * kXcds * ny;
+  // a bf16 gate_up may split its last round: up to n_cu / 8 more workgroups per XCD
+  const int halves = fmt == kBF16 && KIND == kGateUp ? a.n_cu / kXcds : 0;
+  const int blocks = ((tiles + kXcds - 1) / kXcds * ny + halves) * kXcds;
   if (bm != prefill_tile_slots(fmt)) return hipErrorInvalidValue;
 #define L(BF) QMOE_LAUNCH((grouped_gemm<KIND, BF>), dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny)
   switch (fmt) {

@@ -570,6 +570,36 @@ def test_prefill_qwen3_bench_input_full_size():
     assert np.all(np.isfinite(out))
 
 
+def test_prefill_qwen3_first_k_full_size():
+    """The input that bench.py --workload prefill_firstk times: the
+    Qwen3-30B-A3B layer with the reference's own selection (scope = k = 8),
+    so every token goes to experts 0..7 in its own order, T=2048.  These
+    tile counts are known on the host, which runs the gate_up GEMM on half
+    tiles (768 items instead of 384 on 256 CUs).  Every token's ids (exact)
+    and weights (1e-6) against the oracle's router, and 64 rows strided
+    across the batch against the full oracle at the MFMA bar."""
+    cfg = qmoe.CONFIGS["qwen3_30b_a3b"].with_(select_scope=8)
+    announce("prefill qwen3-30b-a3b bf16 T=2048 scope=k, all ids + strided rows vs oracle")
+    hw = qmoe.synthetic_weights(cfg, 2026, quantizer=oracle.host_quantizer)
+    x = qmoe.synthetic_tokens(cfg, 2048, 2026 + 1000)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(x)
+    finally:
+        layer.close()
+    ol = oracle.OracleLayer(hw, scope=8, threads=8)
+    _, rids, rw = ol.router(x)
+    assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
+    assert np.array_equal(np.sort(ids, axis=1), np.tile(np.arange(8), (2048, 1)))
+    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
+    rows = np.arange(5, 2048, 32)
+    ref, _, _ = ol.forward(x[rows])
+    err = rel_err(out[rows], ref)
+    assert err <= TOL_MFMA, f"normwise relative error {err:.3e} > {TOL_MFMA}"
+    assert np.all(np.isfinite(out))
+
+
 def test_prefill_long_prompt_chunked():
     """An 8192-token prompt at k=8: 65536 (token, rank) pairs, more than the
     batched path's slot tables hold, so the forward runs in chunks.  Every
