@@ -628,50 +628,66 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
   }
   wait_vm<0>();  // no LDS-direct load may land after the workgroup ends
 
+  // Epilogue through LDS.  A lane's accumulators hold one slot and runs of
+  // four columns; stored straight to global memory they were 8-byte pieces
+  // of 32 rows a row pitch apart (4.5-9 us per work item).  Each wave writes
+  // its bf16 block (its kRB slots x its columns) into a region of its own in
+  // the rings, rows padded by 16 bytes so that the 8-byte writes to 32 rows
+  // fill the 64 banks twice, and stores it back out in 16-byte chunks along
+  // rows (LDS accesses of one wave complete in order).
+  constexpr int kWCols = KIND == kGateUp ? kBN / 4 : kBN / 2;  // bf16 columns of a wave
+  constexpr int kWPitch = kWCols * 2 + 16;                     // LDS bytes per row of a wave's block
+  constexpr int kWBytes = G::kRB * kWPitch;
+  constexpr int kInA = (int)(sizeof(aring) / kWBytes);         // waves whose blocks fit in the A ring
+  static_assert(kInA + (int)(sizeof(bring) / kWBytes) >= kWaves, "the waves' blocks fit the rings");
+  unsigned char *const wt = w < kInA ? &aring[0][0] + w * kWBytes : &bring[0][0] + (w - kInA) * kWBytes;
+  __syncthreads();  // every wave's fragment reads of the last stages are done
+  auto put4 = [&](int r, int col, const float (&v)[4]) {
+    *reinterpret_cast<uint2 *>(wt + r * kWPitch + col * 2) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+  };
   if constexpr (KIND == kGateUp) {
-    // act = silu(g) * u -> bf16 (model/moe.go:64-75), row pitch Imax
+    // act = silu(g) * u -> bf16 (model/moe.go:64-75); the quotient by its
+    // reciprocal (about an f32 ulp) ahead of the bf16 rounding
 #pragma unroll
-    for (int b = 0; b < G::kNRB; b++) {
-      const int m = wm * G::kRB + b * 32 + l32;
-      if (m < ti.rows) {
-        uint16_t *dst = a.act + (size_t)(ti.slot0 + m) * a.Imax + n0 + wn * 64 + 4 * hi;
+    for (int b = 0; b < G::kNRB; b++)
 #pragma unroll
-        for (int q = 0; q < 2; q++)
+      for (int q = 0; q < 2; q++)
 #pragma unroll
-          for (int j4 = 0; j4 < 4; j4++) {
-            uint16_t h[4];
+        for (int j4 = 0; j4 < 4; j4++) {
+          float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const float g = acc[b][q][4 * j4 + i], u = acc[b][q + 2][4 * j4 + i];
-              const float sgl = g / (1.0f + __expf(-g));
-              h[i] = f32_to_bf16_rne(sgl * u);
-            }
-            *reinterpret_cast<uint2 *>(dst + q * 32 + 8 * j4) =
-                make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+          for (int i = 0; i < 4; i++) {
+            const float g = acc[b][q][4 * j4 + i], u = acc[b][q + 2][4 * j4 + i];
+            v[i] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
           }
-      }
-    }
+          put4(b * 32 + l32, q * 32 + 8 * j4 + 4 * hi, v);
+        }
   } else {
-    // y[slot] = routing weight (or shared gate) * (down . act), stored bf16
+    // y[slot] = routing weight (or shared gate) * (down . act)
 #pragma unroll
     for (int b = 0; b < G::kNRB; b++) {
-      const int m = wm * G::kRB + b * 32 + l32;
-      if (m < ti.rows) {
-        const int slot = ti.slot0 + m;
-        const float ws = a.p.wslot[slot];
-        uint16_t *dst = a.y + (size_t)slot * H + n0 + wn * 128 + 4 * hi;
+      const float ws = a.p.wslot[ti.slot0 + min(wm * G::kRB + b * 32 + l32, ti.rows - 1)];
 #pragma unroll
-        for (int q = 0; q < 4; q++)
+      for (int q = 0; q < 4; q++)
 #pragma unroll
-          for (int j4 = 0; j4 < 4; j4++) {
-            uint16_t h[4];
+        for (int j4 = 0; j4 < 4; j4++) {
+          float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) h[i] = f32_to_bf16_rne(ws * acc[b][q][4 * j4 + i]);
-            *reinterpret_cast<uint2 *>(dst + q * 32 + 8 * j4) =
-                make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
-          }
-      }
+          for (int i = 0; i < 4; i++) v[i] = ws * acc[b][q][4 * j4 + i];
+          put4(b * 32 + l32, q * 32 + 8 * j4 + 4 * hi, v);
+        }
     }
+  }
+  wait_lds_writes();  // the block is in LDS before the wave reads it back
+  constexpr int kCpr = kWCols * 2 / 16;  // 16-byte chunks per row of a wave's block
+  const int nr = min(G::kRB, ti.rows - wm * G::kRB);  // live rows of this wave
+  const size_t pitch = KIND == kGateUp ? (size_t)a.Imax : (size_t)H;
+  uint16_t *const out0 = (KIND == kGateUp ? a.act : a.y) + (size_t)(ti.slot0 + wm * G::kRB) * pitch + n0 + wn * kWCols;
+#pragma unroll
+  for (int i = 0; i < G::kRB * kCpr / 64; i++) {
+    const int c = i * 64 + lane, r = c / kCpr, ch = c % kCpr;
+    if (r < nr)
+      *reinterpret_cast<uint4 *>(out0 + r * pitch + ch * 8) = *reinterpret_cast<const uint4 *>(wt + r * kWPitch + ch * 16);
   }
 }
 
