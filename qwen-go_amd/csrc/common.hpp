@@ -127,4 +127,12 @@ __device__ __forceinline__ void load_chunk(const uint8_t *__restrict__ row, cons
   }
 }
 
+// f32 -> bf16, round to nearest even (NaN stays a NaN): x for the batched
+// GEMMs' A operand.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return (uint16_t)((u >> 16) | 0x40u);  // NaN
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
 }  // namespace qmoe

@@ -43,8 +43,9 @@ struct DevMat {
 // ---- router (router.hip) ----
 // logits (T, E) = x (T, H) @ router^T, each logit one sequential f32 sum in
 // h order with separate multiply and add roundings (model/tensors.go:77-89,
-// model/model.go:167-176).
-hipError_t launch_router_logits(const float *x, int T, const DevMat &router, float *logits,
+// model/model.go:167-176).  xb (T > 32 only; may be null): also store x
+// rounded to bf16, (T, H), for the batched GEMMs.
+hipError_t launch_router_logits(const float *x, int T, const DevMat &router, float *logits, uint16_t *xb,
                                 hipStream_t st);
 // Certified router partials for decode-sized T: sb (T, E, 2) f64 = {S, B}
 // per (token, expert), S ~ exact sum of the reference's f32 products, B a
@@ -194,8 +195,10 @@ bool prefill_supported(int expert_fmt, int H, int I, int Is);
 int prefill_shared_fmt(int shared_fmt);
 int prefill_tile_slots(int expert_fmt);              // slots per GEMM tile for the format
 int prefill_max_tiles(int T, int k, int E, int bm);  // routed tiles, upper bound
+// x_ready: a.xb already holds x in bf16 (the exact router stored it); the
+// prep launch then runs only for the shared gate.
 hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, const float *wts, const float *x,
-                                   const float *shared_gate, float *sg, hipStream_t st);
+                                   const float *shared_gate, float *sg, bool x_ready, hipStream_t st);
 hipError_t launch_prefill_gate_up(const PrefillArgs &a, bool shared, hipStream_t st);
 hipError_t launch_prefill_down(const PrefillArgs &a, bool shared, hipStream_t st);
 hipError_t launch_prefill_combine(const PrefillArgs &a, float *out, hipStream_t st);

@@ -536,6 +536,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
   // partials on the matrix cores, then exact logits of the candidates those
   // leave; otherwise the exact sequential logits of every expert (VALU-bound)
   // and the exact softmax and selection.
+  bool x_ready = false;  // the exact router stored x in bf16 for the GEMMs
   auto route_many = [&]() -> qmoe_status {
     if ((int64_t)T * E >= kCertManyMin && router_cert_mfma_supported(l->router)) {
       STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, ws.sb, st),
@@ -545,7 +546,9 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
             "candidate selection launch");
       return QMOE_OK;
     }
-    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, ws.logits, st), "router logits launch");
+    x_ready = mfma;
+    STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_logits(d_x, T, l->router, ws.logits, mfma ? ws.xb : nullptr, st),
+          "router logits launch");
     STAGE(l, QMOE_STAGE_SELECT, st, launch_softmax_select(ws.logits, T, E, k, l->scope, ids, wts, st),
           "softmax/select launch");
     return QMOE_OK;
@@ -589,7 +592,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
     pa.act = ws.act;
     pa.y = ws.y;
     pa.resid = resid;
-    STAGE(l, QMOE_STAGE_DISPATCH, st, launch_prefill_dispatch(pa, ids, wts, d_x, l->shared_gate, ws.sg, st),
+    STAGE(l, QMOE_STAGE_DISPATCH, st, launch_prefill_dispatch(pa, ids, wts, d_x, l->shared_gate, ws.sg, x_ready, st),
           "dispatch launch");
     STAGE(l, QMOE_STAGE_GATE_UP, st, launch_prefill_gate_up(pa, false, st), "gate_up launch");
     if (Is > 0)

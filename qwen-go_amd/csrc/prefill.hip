@@ -40,12 +40,6 @@ typedef float f32x16_t __attribute__((__vector_size__(16 * sizeof(float))));
 constexpr int kBK = 64;         // K per stage (128 bytes of bf16 per row)
 constexpr int kGemmThreads = 512;
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return (uint16_t)((u >> 16) | 0x40u);  // NaN
-  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-}
-
 // LDS byte offset of the 16-byte chunk c (of 8 k values) of row r in a
 // 128-byte-row tile, XOR-swizzled by the row.  The LDS has 64 banks (256
 // bytes) and serves a 16-byte-per-lane read 16 lanes at a time; those lanes
@@ -745,10 +739,10 @@ int prefill_max_tiles(int T, int k, int E, int bm) {
 }
 
 hipError_t launch_prefill_dispatch(const PrefillArgs &a, const int32_t *ids, const float *wts, const float *x,
-                                   const float *shared_gate, float *sg, hipStream_t st) {
+                                   const float *shared_gate, float *sg, bool x_ready, hipStream_t st) {
   const bool with_shared = a.Is > 0;
-  QMOE_LAUNCH(prep_kernel, dim3(a.T), dim3(256), 0, st, x, a.H, with_shared ? shared_gate : nullptr, a.xb,
-                     sg);
+  if (!x_ready || with_shared)
+    QMOE_LAUNCH(prep_kernel, dim3(a.T), dim3(256), 0, st, x, a.H, with_shared ? shared_gate : nullptr, a.xb, sg);
   const int n = a.T * a.k;
 #define L(J) QMOE_LAUNCH(dispatch_kernel<J>, dim3(1), dim3(kDispatchThreads), 0, st, ids, a.T, a.k, a.E, \
                          (int)with_shared, a.bm, a.bms, a.p)

@@ -54,11 +54,15 @@ __global__ void __launch_bounds__(64) router_rowwise_kernel(const float *__restr
 // and of the router in LDS with k contiguous; the next slice is loaded raw into
 // registers while the current one is multiplied.  Every output sums its
 // products in h order, so the result equals the row-wise kernel's bit for bit.
+// With xb, workgroups past the token tiles (blockIdx.y >= ceil(T / TM), last
+// in dispatch order) only store x rounded to bf16 (the batched GEMMs' A
+// operand), TM tokens each, on the CUs the VALU-bound logit tiles release at
+// their end instead of in a launch of their own.
 template <int FMT, int RM, int RN, int KB>
 __global__ void __launch_bounds__(256) router_tiled_kernel(const float *__restrict__ x, int T, int H,
                                                            const uint8_t *__restrict__ w,
                                                            const uint16_t *__restrict__ s, int E,
-                                                           float *__restrict__ logits) {
+                                                           float *__restrict__ logits, uint16_t *__restrict__ xb) {
 #pragma clang fp contract(off)
   constexpr int TM = 16 * RM, TN = 16 * RN, LD = KB + 4;
   __shared__ __align__(16) float xs[TM][LD];
@@ -66,6 +70,18 @@ __global__ void __launch_bounds__(256) router_tiled_kernel(const float *__restri
   const int tid = threadIdx.x;
   const int tx = tid & 15, ty = tid >> 4;
   const int t0 = blockIdx.y * TM, e0 = blockIdx.x * TN;
+  const int ntok = (T + TM - 1) / TM;
+  if ((int)blockIdx.y >= ntok) {
+    const int c0 = ((blockIdx.y - ntok) * gridDim.x + blockIdx.x) * TM;  // first token of this block
+    const int rows = min(TM, T - c0);
+    for (int i = tid * 4; i < rows * H; i += 256 * 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)c0 * H + i);
+      *reinterpret_cast<uint2 *>(xb + (size_t)c0 * H + i) =
+          make_uint2((uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16),
+                     (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16));
+    }
+    return;
+  }
   constexpr int EPC = Chunk<FMT>::kElems;
   constexpr int CPR = KB / EPC;                        // 16-byte router chunks per row per slice
   constexpr int NXP = TM * KB / 4, NWP = TN * CPR;     // float4 pieces of x, router chunks per slice
@@ -174,7 +190,7 @@ __global__ void __launch_bounds__(256) router_tiled_kernel(const float *__restri
 }
 
 template <int FMT>
-static hipError_t router_logits_fmt(const float *x, int T, const DevMat &r, float *logits,
+static hipError_t router_logits_fmt(const float *x, int T, const DevMat &r, float *logits, uint16_t *xb,
                                     hipStream_t st) {
   const int H = r.cols, E = r.rows;
   if (T <= 32) {
@@ -187,32 +203,36 @@ static hipError_t router_logits_fmt(const float *x, int T, const DevMat &r, floa
     // SIMD, 54 us at one output per lane); 2x2 per lane only once that still
     // gives every CU four workgroups
     const bool wide = (int64_t)T * E >= (int64_t)16 * 256 * 256;
-    const dim3 b(256), g11((E + 15) / 16, (T + 15) / 16), g22((E + 31) / 32, (T + 31) / 32),
-        g12((E + 31) / 32, (T + 15) / 16);
+    // the x conversion rows: ceil(T / TM) blocks of TM tokens after the token tiles
+    auto xrows = [&](int gx, int tm) { return xb ? ((T + tm - 1) / tm + gx - 1) / gx : 0; };
+    const int gx11 = (E + 15) / 16, gx22 = (E + 31) / 32;
+    const dim3 b(256), g11(gx11, (T + 15) / 16 + xrows(gx11, 16)), g22(gx22, (T + 31) / 32 + xrows(gx22, 32)),
+        g12(gx22, (T + 15) / 16 + xrows(gx22, 16));
     if (H % 64 == 0) {
       if (wide)
-        QMOE_LAUNCH((router_tiled_kernel<FMT, 2, 2, 64>), g22, b, 0, st, x, T, H, r.w, r.s, E, logits);
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 2, 2, 64>), g22, b, 0, st, x, T, H, r.w, r.s, E, logits, xb);
       else if (E >= 32)
-        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 2, 64>), g12, b, 0, st, x, T, H, r.w, r.s, E, logits);
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 2, 64>), g12, b, 0, st, x, T, H, r.w, r.s, E, logits, xb);
       else
-        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 1, 64>), g11, b, 0, st, x, T, H, r.w, r.s, E, logits);
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 1, 64>), g11, b, 0, st, x, T, H, r.w, r.s, E, logits, xb);
     } else {
       if (wide)
-        QMOE_LAUNCH((router_tiled_kernel<FMT, 2, 2, 32>), g22, b, 0, st, x, T, H, r.w, r.s, E, logits);
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 2, 2, 32>), g22, b, 0, st, x, T, H, r.w, r.s, E, logits, xb);
       else
-        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 1, 32>), g11, b, 0, st, x, T, H, r.w, r.s, E, logits);
+        QMOE_LAUNCH((router_tiled_kernel<FMT, 1, 1, 32>), g11, b, 0, st, x, T, H, r.w, r.s, E, logits, xb);
     }
   }
   return hipGetLastError();
 }
 
-hipError_t launch_router_logits(const float *x, int T, const DevMat &router, float *logits,
+hipError_t launch_router_logits(const float *x, int T, const DevMat &router, float *logits, uint16_t *xb,
                                 hipStream_t st) {
+  if (xb && T <= 32) return hipErrorInvalidValue;  // only the tiled kernels (T > 32) store xb
   switch (router.fmt) {
-  case kF32: return router_logits_fmt<kF32>(x, T, router, logits, st);
-  case kBF16: return router_logits_fmt<kBF16>(x, T, router, logits, st);
-  case kINT8: return router_logits_fmt<kINT8>(x, T, router, logits, st);
-  default: return router_logits_fmt<kINT4>(x, T, router, logits, st);
+  case kF32: return router_logits_fmt<kF32>(x, T, router, logits, xb, st);
+  case kBF16: return router_logits_fmt<kBF16>(x, T, router, logits, xb, st);
+  case kINT8: return router_logits_fmt<kINT8>(x, T, router, logits, xb, st);
+  default: return router_logits_fmt<kINT4>(x, T, router, logits, xb, st);
   }
 }
 
