@@ -73,9 +73,13 @@ hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, 
 // Selection for T > 32 from the matrix-core partials (bf16 router): exact
 // logits of the candidates the bounds leave, ranked; the exact path for the
 // tokens whose ranks they cannot separate, queued in fbl (1 + T ints).
+// Tokens the candidates cannot settle are queued in fbl and routed on the
+// exact path, each split over several workgroups: qlt holds the logits of the
+// first kExactQueueMax queued tokens, qcnt their workgroup counts.
+constexpr int kExactQueueMax = 64;
 hipError_t launch_select_candidates(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
-                                    int32_t *ids, float *weights, int *fbl, unsigned int *fallbacks,
-                                    hipStream_t st);
+                                    int32_t *ids, float *weights, int *fbl, float *qlt, uint32_t *qcnt,
+                                    unsigned int *fallbacks, hipStream_t st);
 // Certified selection per token from sb, exact fallback on failure.
 hipError_t launch_select_cert(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
                               int32_t *ids, float *weights, unsigned int *fallbacks, hipStream_t st);

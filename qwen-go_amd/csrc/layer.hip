@@ -43,6 +43,8 @@ struct Workspace {
   float *logits = nullptr, *wts = nullptr;
   double *sb = nullptr;
   int *fbl = nullptr;      // {count, tokens} for the exact routing path
+  float *qlt = nullptr;    // (kExactQueueMax, E) exact logits of queued tokens (batched certified routing)
+  uint32_t *qcnt = nullptr;  // (kExactQueueMax) workgroups done per queued token
   int32_t *ids = nullptr;
   // batched (MFMA) path buffers
   uint16_t *xb = nullptr, *act = nullptr;
@@ -387,6 +389,8 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   size_t o_o = take((size_t)nT * d.hidden * 4);
   size_t o_sb = take((size_t)nT * d.n_experts * 16);
   size_t o_fbl = take((size_t)(nT + 1) * 4);      // tokens queued for the exact routing path
+  size_t o_qlt = take((size_t)kExactQueueMax * d.n_experts * 4);
+  size_t o_qcnt = take((size_t)kExactQueueMax * 4);
   size_t o_xn = take((size_t)nT * d.hidden * 4);  // normed x (residual entries)
   const bool want_mfma = mfma || l->ws_mfma;
   const size_t pairs = (size_t)nT * d.top_k, slots = pairs + (size_t)nT;
@@ -433,6 +437,8 @@ qmoe_status ensure_workspace(qmoe_layer *l, int T, hipStream_t user_stream) {
   l->obuf = (float *)(b + o_o);
   w.sb = (double *)(b + o_sb);
   w.fbl = (int *)(b + o_fbl);
+  w.qlt = (float *)(b + o_qlt);
+  w.qcnt = (uint32_t *)(b + o_qcnt);
   w.xn = (float *)(b + o_xn);
   l->ws_mfma = want_mfma;
   if (want_mfma) {
@@ -542,7 +548,8 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
       STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, ws.sb, st),
             "router partials launch");
       STAGE(l, QMOE_STAGE_SELECT, st,
-            launch_select_candidates(d_x, T, l->router, k, l->scope, ws.sb, ids, wts, ws.fbl, l->fallbacks, st),
+            launch_select_candidates(d_x, T, l->router, k, l->scope, ws.sb, ids, wts, ws.fbl, ws.qlt, ws.qcnt,
+                                     l->fallbacks, st),
             "candidate selection launch");
       return QMOE_OK;
     }

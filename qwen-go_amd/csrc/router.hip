@@ -779,40 +779,71 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) se
   if (lane == 0) fbl[1 + atomicAdd(fbl, 1)] = t;
 }
 
-// The exact path for the queued tokens: every logit, a row per thread (x in
-// LDS), then the exact softmax and selection (select_exact_nj).  Workgroup b
-// takes queue entries b, b + gridDim.x, ...
-constexpr int kExactThreads = 512;
+// The exact path for the queued tokens: every logit (the sequential f32 sum,
+// one row per lane), then the exact softmax and selection (select_exact_nj).
+// A queued token's E rows are split over kQSplit workgroups of one wave, so
+// that one token costs about one row's chain instead of every row streamed by
+// one workgroup (C5: 512 rows on one CU took up to 80 us).  Each workgroup
+// stores its logits into the entry's row of qlt and counts itself in
+// qcnt[entry] (release); the last one (acquire) selects.  Entry q is taken by
+// workgroups [kQSplit (q % kQPar), +kQSplit); entries from kQMax on (more than
+// any call queues in practice) are routed whole by one workgroup.
+constexpr int kQSplit = 16, kQPar = 16, kQMax = kExactQueueMax;
 template <int NJ>
-__global__ void __launch_bounds__(kExactThreads) select_exact_kernel(const float *__restrict__ x, DevMat router,
-                                                                     int k, int scope, const int *__restrict__ fbl,
-                                                                     int32_t *__restrict__ ids,
-                                                                     float *__restrict__ weights,
-                                                                     unsigned int *__restrict__ fallbacks) {
+__global__ void __launch_bounds__(64) select_exact_kernel(const float *__restrict__ x, DevMat router, int k,
+                                                          int scope, const int *__restrict__ fbl,
+                                                          float *__restrict__ qlt, uint32_t *__restrict__ qcnt,
+                                                          int32_t *__restrict__ ids, float *__restrict__ weights,
+                                                          unsigned int *__restrict__ fallbacks) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int E = router.rows, H = router.cols, n = fbl[0];
+  __shared__ int s_last;
+  const int E = router.rows, H = router.cols, n = fbl[0], lane = threadIdx.x;
   float *xs = reinterpret_cast<float *>(smem);
   float *lt = xs + H;
-  for (int q = blockIdx.x; q < n; q += gridDim.x) {
-    const int t = fbl[1 + q];
+  const int part = blockIdx.x % kQSplit, slot = blockIdx.x / kQSplit;
+  const int per = (E + kQSplit - 1) / kQSplit;  // rows of a part (<= 64: E <= 1024)
+  auto load_x = [&](int t) {
     __syncthreads();  // the previous entry's LDS reads are done
-    for (int i = threadIdx.x; i < H; i += kExactThreads) xs[i] = x[(size_t)t * H + i];
+    for (int i = lane * 4; i < H; i += 256)
+      *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(x + (size_t)t * H + i);
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += kExactThreads)
-      // one or two queued tokens per call: latency-bound, so 16 chunks in flight
-      lt[e] = exact_row_logit<kBF16, 16>(xs, H, router.w + (size_t)e * H * 2, nullptr);
+  };
+  for (int q = slot; q < n; q += kQPar) {
+    const int t = fbl[1 + q];
+    int32_t *gi = ids + (size_t)t * k;
+    float *gw = weights + (size_t)t * k;
+    if (q >= kQMax) {  // whole token in one workgroup (part 0)
+      if (part != 0) continue;
+      load_x(t);
+      for (int e = lane; e < E; e += 64) lt[e] = exact_row_logit<kBF16, 16>(xs, H, router.w + (size_t)e * H * 2, nullptr);
+      __syncthreads();
+      select_exact_nj<NJ>(lt, E, k, scope, gi, gw, nullptr, nullptr);
+      if (lane == 0) atomicAdd(fallbacks, 1u);
+      continue;
+    }
+    load_x(t);
+    const int e = part * per + lane;
+    if (lane < per && e < E)
+      qlt[(size_t)q * E + e] = exact_row_logit<kBF16, 16>(xs, H, router.w + (size_t)e * H * 2, nullptr);
+    __threadfence();  // release this part's logits
+    if (lane == 0) s_last = atomicAdd(qcnt + q, 1u) == kQSplit - 1;
     __syncthreads();
-    if (threadIdx.x < 64) {
-      select_exact_nj<NJ>(lt, E, k, scope, ids + (size_t)t * k, weights + (size_t)t * k, nullptr, nullptr);
-      if (threadIdx.x == 0) atomicAdd(fallbacks, 1u);
+    if (s_last) {
+      __threadfence();  // acquire every part's logits
+      for (int i = lane; i < E; i += 64) lt[i] = __hip_atomic_load(qlt + (size_t)q * E + i, __ATOMIC_RELAXED,
+                                                                      __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      select_exact_nj<NJ>(lt, E, k, scope, gi, gw, nullptr, nullptr);
+      if (lane == 0) atomicAdd(fallbacks, 1u);
     }
   }
 }
 
 hipError_t launch_select_candidates(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
-                                    int32_t *ids, float *weights, int *fbl, unsigned int *fallbacks,
-                                    hipStream_t st) {
+                                    int32_t *ids, float *weights, int *fbl, float *qlt, uint32_t *qcnt,
+                                    unsigned int *fallbacks, hipStream_t st) {
   hipError_t e = launch_zero(reinterpret_cast<float *>(fbl), 1, st);  // the queue's count (0 bits)
+  if (e == hipSuccess) e = launch_zero(reinterpret_cast<float *>(qcnt), kQMax, st);
   if (e != hipSuccess) return e;
   const size_t lds = (size_t)router.cols * 4;
 #define L(NJ) QMOE_LAUNCH(select_candidates_kernel<NJ>, dim3(T), dim3(64), lds, st, x, router, k, scope, sb, ids, \
@@ -820,9 +851,8 @@ hipError_t launch_select_candidates(const float *x, int T, const DevMat &router,
   QMOE_NJ_DISPATCH(router.rows, L);
 #undef L
   const size_t lds2 = (size_t)router.cols * 4 + (size_t)router.rows * 4;
-  const int blocks = T < 256 ? T : 256;
-#define L(NJ) QMOE_LAUNCH(select_exact_kernel<NJ>, dim3(blocks), dim3(kExactThreads), lds2, st, x, router, k, scope, \
-                          fbl, ids, weights, fallbacks)
+#define L(NJ) QMOE_LAUNCH(select_exact_kernel<NJ>, dim3(kQSplit * kQPar), dim3(64), lds2, st, x, router, k, scope, \
+                          fbl, qlt, qcnt, ids, weights, fallbacks)
   QMOE_NJ_DISPATCH(router.rows, L);
 #undef L
   return hipGetLastError();

@@ -733,6 +733,34 @@ def test_batched_router_candidates_ties():
     assert fb == 0, fb
 
 
+def test_batched_router_exact_queue():
+    """2048 tokens x 512 experts with one router row scaled by 100: for many
+    tokens that expert's logit lies more than 80 above the other selected
+    ones, whose probabilities then underflow, which only the exact path
+    settles.  Those tokens are queued; the first 64 are routed by workgroups
+    that each take a share of the experts, the rest whole by one workgroup.
+    ids and weights against the oracle's router for every token."""
+    cfg = qmoe.LayerConfig(2048, 512, 8, 64, 0, 512, qmoe.BF16, qmoe.BF16, qmoe.BF16, "exact-queue")
+    announce("batched router exact queue, T=2048 E=512, one row x100")
+    hw = qmoe.synthetic_weights(cfg, 93, quantizer=oracle.host_quantizer)
+    r = qmoe.bf16_bits_to_f32(hw.router).reshape(512, 2048)
+    r[7] *= 100.0
+    hw.router = qmoe.f32_to_bf16_bits(r.reshape(-1)).reshape(hw.router.shape)
+    x = qmoe.synthetic_tokens(cfg, 2048, 93)
+    layer = qmoe.MoeLayer(cfg)
+    try:
+        hw.upload(layer)
+        out, ids, w = layer.forward(x)
+        fb = layer.router_fallbacks()
+    finally:
+        layer.close()
+    _, rids, rw = oracle.OracleLayer(hw, threads=8).router(x)
+    assert np.array_equal(ids, rids), f"ids differ at {np.argwhere(ids != rids)[:5]}"
+    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=0)
+    assert fb > 64, fb
+    assert np.all(np.isfinite(out))
+
+
 def test_decode_exchange_timeout_fails_that_call():
     """The T = 1 kernel's workgroups exchange router partials with a bounded
     wait.  With the wait budget set to zero from the host, every wait gives up
