@@ -639,28 +639,38 @@ hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, 
 // Weights: e_r = fl(exp(fl(L_r - max))) as the reference rounds it, divided by
 // the f64 softmax sum of the partials over all E, renormalised with moe.go:63's
 // 1e-9.
+// Two tokens per workgroup, one wave each for the bounds, the candidates and
+// the certification; the exact logits of both tokens' candidates are computed
+// lane-packed in between (by wave 0 alone when they fit 64 lanes), since a
+// wave's VALU instructions cost the same however few lanes run the chains.
+constexpr int kCandTokens = 2;
 template <int NJ>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) select_candidates_kernel(const float *__restrict__ x, DevMat router, int k,
-                                                               int scope, const double *__restrict__ sb,
-                                                               int32_t *__restrict__ ids, float *__restrict__ weights,
-                                                               int *__restrict__ fbl) {
+__global__ void __launch_bounds__(64 * kCandTokens) __attribute__((amdgpu_waves_per_eu(4)))
+    select_candidates_kernel(const float *__restrict__ x, int T, DevMat router, int k, int scope,
+                             const double *__restrict__ sb, int32_t *__restrict__ ids, float *__restrict__ weights,
+                             int *__restrict__ fbl) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int list[64], sorted_e[64];
-  __shared__ float sorted_l[64];
-  const int t = blockIdx.x, lane = threadIdx.x;
+  __shared__ int list_all[kCandTokens][64], sorted_e_all[kCandTokens][64], ncand[kCandTokens];
+  __shared__ float sorted_l_all[kCandTokens][64], cand_l[kCandTokens][64];
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kCandTokens + wv;
+  const bool live = t < T;
   const int E = router.rows, H = router.cols;
-  float *xs = reinterpret_cast<float *>(smem);
-  for (int i = lane * 4; i < H; i += 256)
-    *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(x + (size_t)t * H + i);
+  int *list = list_all[wv], *sorted_e = sorted_e_all[wv];
+  float *sorted_l = sorted_l_all[wv];
+  float *xs = reinterpret_cast<float *>(smem) + (size_t)wv * H;
+  if (live)
+    for (int i = lane * 4; i < H; i += 256)
+      *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(x + (size_t)t * H + i);
   double S[NJ], B[NJ];
   float key[NJ];       // lower bounds in the scope, rounded down to f32
   double glo = -INFINITY;  // the largest lower bound over all E
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
     const int e = lane + 64 * j;
-    const double2 v = e < E ? reinterpret_cast<const double2 *>(sb + (size_t)t * E * 2)[e]
-                            : make_double2(-INFINITY, 0.0);
+    const double2 v = live && e < E ? reinterpret_cast<const double2 *>(sb + (size_t)t * E * 2)[e]
+                                    : make_double2(-INFINITY, 0.0);
     S[j] = v.x;
     B[j] = v.y;
     const double lo = S[j] - B[j];
@@ -704,29 +714,42 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) se
   }
   // candidates, compacted into list: in the scope with upper bound >= lo_k,
   // or (any index) with upper bound >= glo, which includes the maximum's expert
-  bool in[NJ];
   int n = 0;
   double uo = -INFINITY;  // the largest upper bound among the scope's others
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
     const int e = lane + 64 * j;
     const double up = S[j] + B[j];
-    in[j] = e < E && ((e < scope && up >= (double)lo_k) || up >= glo);
-    const uint64_t m = __ballot(in[j]);
+    const bool in = e < E && ((e < scope && up >= (double)lo_k) || up >= glo);
+    const uint64_t m = __ballot(in);
     const int idx = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-    if (in[j] && idx < 64) list[idx] = e;
+    if (in && idx < 64) list[idx] = e;
     n += __popcll(m);
-    if (!in[j] && e < scope && e < E) uo = fmax(uo, up);
+    if (!in && e < scope && e < E) uo = fmax(uo, up);
   }
   uo = wave_max_f64(uo);
-  bool ok = n <= 64;
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  bool ok = live && n <= 64;
+  if (lane == 0) ncand[wv] = ok ? n : 0;
+  __syncthreads();  // every wave's x, list and count
+  // the exact reference logits of every candidate, lane-packed over the block
+  {
+    int g = threadIdx.x, tw = -1;
+#pragma unroll
+    for (int q = 0; q < kCandTokens; q++) {
+      if (tw < 0 && g < ncand[q]) tw = q;
+      else if (tw < 0) g -= ncand[q];
+    }
+    if (tw >= 0)
+      cand_l[tw][g] = exact_row_logit<kBF16>(reinterpret_cast<const float *>(smem) + (size_t)tw * H, H,
+                                            router.w + (size_t)list_all[tw][g] * H * 2, nullptr);
+  }
+  __syncthreads();
   if (ok) {
     float L = -INFINITY;
     int ce = 0x7fffffff;
     if (lane < n) {
       ce = list[lane];
-      L = exact_row_logit<kBF16>(xs, H, router.w + (size_t)ce * H * 2, nullptr);
+      L = cand_l[wv][lane];
     }
     // the reference's maximum over all E logits (its expert is listed)
     const float Lmax = wave_max_f32(L);
@@ -776,7 +799,7 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) se
     }
   }
   // queued for the exact path
-  if (lane == 0) fbl[1 + atomicAdd(fbl, 1)] = t;
+  if (live && lane == 0) fbl[1 + atomicAdd(fbl, 1)] = t;
 }
 
 // The exact path for the queued tokens: every logit (the sequential f32 sum,
@@ -845,9 +868,9 @@ hipError_t launch_select_candidates(const float *x, int T, const DevMat &router,
   hipError_t e = launch_zero(reinterpret_cast<float *>(fbl), 1, st);  // the queue's count (0 bits)
   if (e == hipSuccess) e = launch_zero(reinterpret_cast<float *>(qcnt), kQMax, st);
   if (e != hipSuccess) return e;
-  const size_t lds = (size_t)router.cols * 4;
-#define L(NJ) QMOE_LAUNCH(select_candidates_kernel<NJ>, dim3(T), dim3(64), lds, st, x, router, k, scope, sb, ids, \
-                          weights, fbl)
+  const size_t lds = (size_t)router.cols * 4 * kCandTokens;
+#define L(NJ) QMOE_LAUNCH(select_candidates_kernel<NJ>, dim3((T + kCandTokens - 1) / kCandTokens), \
+                          dim3(64 * kCandTokens), lds, st, x, T, router, k, scope, sb, ids, weights, fbl)
   QMOE_NJ_DISPATCH(router.rows, L);
 #undef L
   const size_t lds2 = (size_t)router.cols * 4 + (size_t)router.rows * 4;
