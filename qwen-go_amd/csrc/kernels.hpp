@@ -69,13 +69,17 @@ hipError_t launch_router_sb(const float *x, int T, const DevMat &router, double 
 // multiple of 64, at most 8192): the same sb as launch_router_sb, from x split
 // into exact bf16 parts inside the kernel.
 bool router_cert_mfma_supported(const DevMat &router);
-hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, double *sb, hipStream_t st);
+// fbl / qcnt (may be null): the exact queue of launch_select_candidates,
+// cleared by this launch for the selection after it.
+hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, double *sb, int *fbl,
+                                   uint32_t *qcnt, hipStream_t st);
 // Selection for T > 32 from the matrix-core partials (bf16 router): exact
 // logits of the candidates the bounds leave, ranked; the exact path for the
 // tokens whose ranks they cannot separate, queued in fbl (1 + T ints).
 // Tokens the candidates cannot settle are queued in fbl and routed on the
 // exact path, each split over several workgroups: qlt holds the logits of the
-// first kExactQueueMax queued tokens, qcnt their workgroup counts.
+// first kExactQueueMax queued tokens, qcnt their workgroup counts.  fbl[0]
+// and qcnt must be zero on entry (launch_router_cert_mfma clears them).
 constexpr int kExactQueueMax = 64;
 hipError_t launch_select_candidates(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
                                     int32_t *ids, float *weights, int *fbl, float *qlt, uint32_t *qcnt,

@@ -545,7 +545,7 @@ qmoe_status run_forward(qmoe_layer *l, const Workspace &ws, const float *d_x, in
   bool x_ready = false;  // the exact router stored x in bf16 for the GEMMs
   auto route_many = [&]() -> qmoe_status {
     if ((int64_t)T * E >= kCertManyMin && router_cert_mfma_supported(l->router)) {
-      STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, ws.sb, st),
+      STAGE(l, QMOE_STAGE_ROUTER, st, launch_router_cert_mfma(d_x, T, l->router, ws.sb, ws.fbl, ws.qcnt, st),
             "router partials launch");
       STAGE(l, QMOE_STAGE_SELECT, st,
             launch_select_candidates(d_x, T, l->router, k, l->scope, ws.sb, ids, wts, ws.fbl, ws.qlt, ws.qcnt,
@@ -1197,7 +1197,7 @@ qmoe_status qmoe_router_bounds_debug(qmoe_layer *l, const float *x, int32_t T, d
   hipError_t e = hipMemcpyAsync(l->xbuf, x, nx * 4, hipMemcpyHostToDevice, l->stream);
   if (e == hipSuccess)
     e = small ? launch_router_sb(l->xbuf, T, l->router, l->w.sb, nullptr, nullptr, RouterNorm{}, l->stream)
-              : launch_router_cert_mfma(l->xbuf, T, l->router, l->w.sb, l->stream);
+              : launch_router_cert_mfma(l->xbuf, T, l->router, l->w.sb, nullptr, nullptr, l->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(sb_out, l->w.sb, nsb * 8, hipMemcpyDeviceToHost, l->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(l->stream);
   if (e != hipSuccess) return hip_fail(l, e, "router_bounds_debug");

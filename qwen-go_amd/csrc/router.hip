@@ -533,12 +533,19 @@ __device__ __forceinline__ void cert_fold(cert_f32x16 (&acc)[2], float (&S)[16],
 // loads 8 f32 of x (two blocks ahead) and stores those 8 elements of all four
 // pieces; each wave keeps its router fragments in registers, loaded two blocks
 // ahead.
+// With qzero, workgroup (0, 0) also clears the selection's exact queue (its
+// count and the first nq per-token workgroup counts) for the launches after it.
 __global__ void __launch_bounds__(256, 1) router_cert_mfma_kernel(const float *__restrict__ x, int T, int H,
                                                                const uint16_t *__restrict__ w, int E,
-                                                               double *__restrict__ sb) {
+                                                               double *__restrict__ sb, int *__restrict__ fbl,
+                                                               uint32_t *__restrict__ qcnt, int nq) {
 #pragma clang fp contract(off)
   __shared__ __align__(16) uint16_t at[2][4][32 * kCertPitch];
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hi = lane >> 5;
+  if (fbl && blockIdx.x == 0 && blockIdx.y == 0) {
+    if (tid == 0) fbl[0] = 0;
+    for (int i = tid; i < nq; i += 256) qcnt[i] = 0;
+  }
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t0 = blockIdx.y * 32;
   const int ew0 = blockIdx.x * 128 + wv * 32;  // first expert of this wave (uniform)
@@ -611,15 +618,16 @@ bool router_cert_mfma_supported(const DevMat &router) {
   return router.fmt == kBF16 && router.cols % 64 == 0 && router.cols <= 8192 && router.rows <= kMaxE;
 }
 
-hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, double *sb, hipStream_t st) {
+hipError_t launch_router_cert_mfma(const float *x, int T, const DevMat &router, double *sb, int *fbl,
+                                   uint32_t *qcnt, hipStream_t st) {
   const int H = router.cols, E = router.rows;
   QMOE_LAUNCH(router_cert_mfma_kernel, dim3((E + 127) / 128, (T + 31) / 32), dim3(256), 0, st, x, T, H,
-              reinterpret_cast<const uint16_t *>(router.w), E, sb);
+              reinterpret_cast<const uint16_t *>(router.w), E, sb, fbl, qcnt, fbl ? kExactQueueMax : 0);
   return hipGetLastError();
 }
 
 // Selection for many tokens from the matrix-core partials (bf16 router), one
-// wavefront per token.  lo_k = the k-th largest lower bound S - B among the
+// wavefront per token for everything but the exact logits.  lo_k = the k-th largest lower bound S - B among the
 // experts of the scope; every expert of the scope whose upper bound S + B
 // reaches it (the true top k of the scope are among them) gets its reference
 // logit computed exactly, one per lane (the sequential f32 sum of
@@ -865,9 +873,6 @@ __global__ void __launch_bounds__(64) select_exact_kernel(const float *__restric
 hipError_t launch_select_candidates(const float *x, int T, const DevMat &router, int k, int scope, const double *sb,
                                     int32_t *ids, float *weights, int *fbl, float *qlt, uint32_t *qcnt,
                                     unsigned int *fallbacks, hipStream_t st) {
-  hipError_t e = launch_zero(reinterpret_cast<float *>(fbl), 1, st);  // the queue's count (0 bits)
-  if (e == hipSuccess) e = launch_zero(reinterpret_cast<float *>(qcnt), kQMax, st);
-  if (e != hipSuccess) return e;
   const size_t lds = (size_t)router.cols * 4 * kCandTokens;
 #define L(NJ) QMOE_LAUNCH(select_candidates_kernel<NJ>, dim3((T + kCandTokens - 1) / kCandTokens), \
                           dim3(64 * kCandTokens), lds, st, x, T, router, k, scope, sb, ids, weights, fbl)
