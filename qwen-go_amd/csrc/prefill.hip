@@ -359,12 +359,12 @@ __device__ __forceinline__ void dma4(const void *src, const unsigned char *lds_w
 // tile's A rows in the same L2.
 //
 // A workgroup holds a CU (its LDS), so an XCD runs its n items in rounds of
-// cus = n_cu / 8.  For a bf16 gate_up, a last round of at most cus / 2 items
-// runs as twice as many half items: slots [0, 128) and [128, 256) of the tile
-// in two workgroups, each with only waves 0-3 (the first ping-pong group)
-// issuing MFMAs, which takes about 0.67 of a full item's time (C = k, T = 2048
-// at Qwen3-30B: 48 items per XCD as 32 full + 32 halves instead of two full
-// rounds).
+// cus = n_cu / 8.  For a gate_up, a last round of at most cus / 2 items runs
+// as twice as many half items: the two halves of the tile's slots in two
+// workgroups, each with only the waves of its half issuing MFMAs, which takes
+// about 0.9 of a full item's time (bf16, C = k, T = 2048 at Qwen3-30B: 48
+// items per XCD as 32 full + 32 halves instead of two full rounds).  The
+// group-32 formats split only a launch that is one part-filled round.
 constexpr int kXcds = 8;
 
 template <int KIND, int BF>
@@ -380,9 +380,13 @@ __global__ void __launch_bounds__(kGemmThreads) grouped_gemm(PrefillArgs a, int 
   const int per_xcd = (nt + kXcds - 1) / kXcds;
   const int n = per_xcd * ny;  // items of this XCD
   int split_from = n;          // items from here on run as two half items
-  if constexpr (BF == kBF16 && KIND == kGateUp) {
+  if constexpr (KIND == kGateUp) {
+    // the group-32 formats (lockstep, every wave dequantising the B tile)
+    // gain only when the whole launch is one part-filled round (C5's shared
+    // expert: 16 items per XCD, 52 -> 43 us); a last round of more items got
+    // slower
     const int cus = a.n_cu / kXcds, rem = cus > 0 ? n % cus : 0;
-    if (rem > 0 && 2 * rem <= cus) split_from = n - rem;
+    if (rem > 0 && 2 * rem <= cus && (BF == kBF16 || rem == n)) split_from = n - rem;
   }
   int item = j, half = -1;
   if (j >= split_from) {
@@ -762,7 +766,7 @@ static hipError_t gemm_launch(const PrefillArgs &a, bool shared, int ny, hipStre
   const int fmt = shared ? a.sfmt : a.fmt, bm = shared ? a.bms : a.bm;
   const int tiles = shared ? (a.T + bm - 1) / bm : prefill_max_tiles(a.T, a.k, a.E, bm);
   // a bf16 gate_up may split its last round: up to n_cu / 8 more workgroups per XCD
-  const int halves = fmt == kBF16 && KIND == kGateUp ? a.n_cu / kXcds : 0;
+  const int halves = KIND == kGateUp ? a.n_cu / kXcds : 0;
   const int blocks = ((tiles + kXcds - 1) / kXcds * ny + halves) * kXcds;
   if (bm != prefill_tile_slots(fmt)) return hipErrorInvalidValue;
 #define L(BF) QMOE_LAUNCH((grouped_gemm<KIND, BF>), dim3(blocks), dim3(kGemmThreads), 0, st, a, (int)shared, ny)
