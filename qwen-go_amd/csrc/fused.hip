@@ -43,6 +43,7 @@ constexpr int kBurstKB = 16;
 __host__ __device__ inline size_t fused_head_bytes(int H, int E) {
   return ((size_t)(3 * H + E) * 4 + 15) / 16 * 16;
 }
+constexpr uint64_t kRankGapTicks = 40;         // 0.4 us at the 100 MHz s_memrealtime clock
 constexpr size_t kLdsLimit = 160 * 1024 - 2048;  // static LDS < 1 KiB
 
 // Waits until the n tagged words (one per workgroup, saying that its slice of
@@ -794,6 +795,12 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
     while (__hip_atomic_load(&s_spec[rk], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
       __builtin_amdgcn_s_sleep(1);
   }
+  // T = 1: a rank's bursts start rank * rank_gap ticks after its expert is
+  // known, spreading the ranks' reads beyond the selection rounds' own spacing
+  if (a.rank_gap && rank0 != a.k) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime(), d = (uint64_t)rank0 * a.rank_gap;
+    while (__builtin_amdgcn_s_memrealtime() - t0 < d) __builtin_amdgcn_s_sleep(1);
+  }
   QMOE_STAMP(5, 1);
   QMOE_STAMP(12, 7);
   te0 = run_expert(0, true);
@@ -885,6 +892,12 @@ static void fused_launch(const FusedArgs &a0, hipStream_t st) {
   FusedArgs a = a0;
   const int blocks = fused_grid(a);
   a.burst = fused_burst_fits(a.H, a.E);
+  // Same-box A/B of the gap (0.1 us steps): at T = 1 with the in-kernel router
+  // and ranks of several MB (Qwen3-30B-A3B: bf16 9.4 MB, int8 4.7 MB per rank)
+  // 0.4 us ends the data phase sooner (bf16 29.8 -> 28.9 us, int8 26.8 -> 26.2);
+  // with 1.5 MB ranks (int4, E = 512) or at T = 8 any gap is slower.
+  a.rank_gap = a.fused_router && a.T == 1 && fmt_matrix_bytes(a.fmt, 3 * a.I, a.H) >= (int64_t)(4 << 20)
+                   ? kRankGapTicks : 0;
   const size_t lds = fused_lds_bytes(a.H, a.E);
   if (a.occ_out) {
     *a.occ_out = 0;

@@ -122,6 +122,7 @@ struct FusedArgs {
   int n_cu;                           // compute units of the device
   int nb, rb;                         // filled by the launcher: blocks per token, rows per block
   int burst;                          // filled by the launcher: LDS holds the burst-mode down rows
+  uint64_t rank_gap;                  // filled by the launcher: s_memrealtime ticks between ranks' bursts
   // T = 1, bf16 router: the kernel computes the router partials itself
   // (fused_router = router chunks per lane, 1, 2 or 4; sb null), exchanges
   // them between its workgroups through rtag (one word per expert) tagged with
