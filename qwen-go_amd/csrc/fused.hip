@@ -857,10 +857,18 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   float *out_t = a.out + (size_t)t * H;
   // output order: the global atomics of a wave then cover 256 contiguous bytes
   const int rot = H % 64 == 0 ? (int)(blockIdx.x % (H / 64)) * 64 : 0;
+  // In burst mode red holds only recomputed runs: read it only then (its
+  // element-major reads in output order put EPC consecutive outputs in one
+  // LDS bank, an EPC-way conflict)
+  const bool red_live = !use_burst || redo != 0;
   for (int j0 = threadIdx.x; j0 < H; j0 += kFusedBlock) {
     const int j = j0 + rot < H ? j0 + rot : j0 + rot - H;
-    const int pj = pos(j / EPC, j % EPC);
-    float s0 = red[pj], s1 = red[H + pj];
+    float s0 = 0.0f, s1 = 0.0f;
+    if (red_live) {
+      const int pj = pos(j / EPC, j % EPC);
+      s0 = red[pj];
+      s1 = red[H + pj];
+    }
     if (use_burst)  // burst sums are stored in output order
       for (int w = 0; w < kFusedBlock / 64; w++) {
         const float *part = reinterpret_cast<const float *>(burst_lds + (size_t)w * kBurstKB * 1024);
