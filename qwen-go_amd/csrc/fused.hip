@@ -308,23 +308,6 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   const int dt = threadIdx.x;  // row-streaming thread index (all threads)
   const bool writer = blockIdx.x % a.nb == 0 && (a.sb || a.fused_router) && a.k_routed > 0;
 
-  if (threadIdx.x < 64) s_spec[threadIdx.x] = 0;
-  if (threadIdx.x == 0) s_xready = fnorm ? (kFusedBlock - kCtl) / 64 : 0;  // the prologue filled xs
-  for (int j = threadIdx.x; j < 2 * H; j += kFusedBlock) red[j] = 0.0f;
-  __syncthreads();
-  // Waves 1..7 load x[t] into LDS and count themselves done in s_xready; the
-  // control wave starts the selection at once, without x.
-  if (!ctl && !fnorm) {
-    for (int i = (threadIdx.x - kCtl) * 4; i < H; i += (kFusedBlock - kCtl) * 4)
-      *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.x + (size_t)t * H + i);
-    if ((threadIdx.x & 63) == 0)
-      __hip_atomic_fetch_add(&s_xready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  auto wait_x = [&]() {
-    while (__hip_atomic_load(&s_xready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < (kFusedBlock - kCtl) / 64)
-      __builtin_amdgcn_s_sleep(1);
-  };
-
   // ---- geometry of a row: nch 16-byte chunks, lpr lanes per row
   const int64_t row_bytes = fmt_matrix_bytes(FMT, 1, H);  // gate/up rows and transposed down rows
   const int gnsc = H / kGroup;
@@ -352,6 +335,32 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
   // in plain order, no better.)
   const bool pswz = EPC >= 16 && H % 64 == 0;
   auto part_idx = [&](int j) { return pswz ? j ^ (((j >> 6) & 15) << 2) : j; };
+  // Burst mode with that swizzle: the data waves also store x, swizzled the
+  // same way, into red (the burst keeps its sums elsewhere; a recompute clears
+  // red first), where each lane's EPC consecutive x values read without bank
+  // conflicts.
+  const bool xcopy = use_burst && pswz && !fnorm;
+
+  if (threadIdx.x < 64) s_spec[threadIdx.x] = 0;
+  if (threadIdx.x == 0) s_xready = fnorm ? (kFusedBlock - kCtl) / 64 : 0;  // the prologue filled xs
+  for (int j = threadIdx.x; j < 2 * H; j += kFusedBlock) red[j] = 0.0f;
+  __syncthreads();
+  // Waves 1..7 load x[t] into LDS and count themselves done in s_xready; the
+  // control wave starts the selection at once, without x.
+  if (!ctl && !fnorm) {
+    for (int i = (threadIdx.x - kCtl) * 4; i < H; i += (kFusedBlock - kCtl) * 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(a.x + (size_t)t * H + i);
+      *reinterpret_cast<float4 *>(xs + i) = v;
+      if (xcopy) *reinterpret_cast<float4 *>(red + part_idx(i)) = v;
+    }
+    if ((threadIdx.x & 63) == 0)
+      __hip_atomic_fetch_add(&s_xready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  auto wait_x = [&]() {
+    while (__hip_atomic_load(&s_xready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < (kFusedBlock - kCtl) / 64)
+      __builtin_amdgcn_s_sleep(1);
+  };
+
   const int rs = g < 0 ? 0 : (int)((int64_t)g * nrows / groups);
   const int re = g < 0 ? 0 : (int)((int64_t)(g + 1) * nrows / groups);
 
@@ -508,6 +517,22 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
 #pragma unroll
             for (int c = 0; c < IT; c++) asm volatile("" : "+v"(bgs[r][c]), "+v"(bus[r][c]));
         }
+        // this lane's x chunks, read once for all its rows
+        const float *xb = xcopy ? red : xs;
+        float xl[IT][EPC];
+#pragma unroll
+        for (int c = 0; c < IT; c++) {
+          const int j0 = (sl + c * lpr) * EPC;
+#pragma unroll
+          for (int q = 0; q < EPC / 4; q++) {
+            const int xi = xcopy ? part_idx(j0 + 4 * q) : j0 + 4 * q;
+            const float4 v = *reinterpret_cast<const float4 *>(xb + xi);
+            xl[c][4 * q] = v.x;
+            xl[c][4 * q + 1] = v.y;
+            xl[c][4 * q + 2] = v.z;
+            xl[c][4 * q + 3] = v.w;
+          }
+        }
         float act[BR];
 #pragma unroll
         for (int r = 0; r < BR; r++) {
@@ -516,9 +541,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
             float gv = 0.0f, uv = 0.0f;
 #pragma unroll
             for (int c = 0; c < IT; c++) {
-              const int ch = sl + c * lpr;
-              float dg = chunk_dot<FMT>(bg[r][c], xs + ch * EPC);
-              float du = chunk_dot<FMT>(bu[r][c], xs + ch * EPC);
+              float dg = chunk_dot<FMT>(bg[r][c], xl[c]);
+              float du = chunk_dot<FMT>(bu[r][c], xl[c]);
               if constexpr (fmt_quant(FMT)) {
                 dg *= f16_to_f32((uint16_t)bgs[r][c]);
                 du *= f16_to_f32((uint16_t)bus[r][c]);
@@ -847,8 +871,8 @@ __global__ void __launch_bounds__(kFusedBlock) expert_fused_kernel(FusedArgs a) 
     // recompute the runs in `redo` into red (streaming mode); their burst
     // partial sums are dropped
     for (int j = threadIdx.x; j < H; j += kFusedBlock) {
-      if (redo & 1) red[j] = 0.0f;
-      if (redo & 2) red[H + j] = 0.0f;
+      if ((redo & 1) || use_burst) red[j] = 0.0f;  // burst mode: red holds nothing (x, with xcopy)
+      if ((redo & 2) || use_burst) red[H + j] = 0.0f;
       if (use_burst)
         for (int w = 0; w < kFusedBlock / 64; w++) {
           float *part = reinterpret_cast<float *>(burst_lds + (size_t)w * kBurstKB * 1024);
